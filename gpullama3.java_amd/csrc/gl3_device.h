@@ -1,0 +1,150 @@
+// Device-side building blocks of the gfx950 decode path: fp16 conversion,
+// wavefront reductions, coherent loads/stores for data exchanged between
+// workgroups, and the grid barrier of the persistent per-token kernel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define GL3_WAVE 64
+#define GL3_BLOCK 256
+#define GL3_WAVES_PER_BLOCK (GL3_BLOCK / GL3_WAVE)
+
+namespace gl3 {
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------- fp16
+
+// Exact binary16 -> binary32 (subnormals preserved: fp16 denormals are not
+// flushed on gfx950 in the default float mode).
+__device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+__device__ __forceinline__ float h2f_lo(unsigned w) { return h2f((uint16_t)(w & 0xffffu)); }
+__device__ __forceinline__ float h2f_hi(unsigned w) { return h2f((uint16_t)(w >> 16)); }
+// binary32 -> binary16, round to nearest even
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+// signed byte k of w as float (one v_cvt_f32_i32_sdwa with sext, src0_sel:BYTE_k)
+template <int K>
+__device__ __forceinline__ float sbyte(unsigned w) { return (float)(signed char)((w >> (8 * K)) & 0xffu); }
+
+// ------------------------------------------------- coherent data exchange
+// Activations written by one workgroup and read by another inside the same
+// kernel go through agent-scope relaxed atomics: they bypass the per-XCD L2
+// (which is not coherent across XCDs) without the cost of a release fence.
+
+__device__ __forceinline__ float ld_coherent(const float *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coherent(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned ld_coherent_u32(const unsigned *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coherent_u32(unsigned *p, unsigned v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int ld_coherent_i32(const int *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long ld_coherent_u64(const unsigned long long *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Wait until this wave's outstanding vector-memory operations (including the
+// coherent stores above) have completed.  Used instead of a release fence
+// before signalling another workgroup.
+__device__ __forceinline__ void vmem_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Streaming (read-once) 16-byte load of weights / KV.
+__device__ __forceinline__ u32x4 ld_stream(const void *p) { return __builtin_nontemporal_load((const u32x4 *)p); }
+
+// ------------------------------------------------------------ reductions
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the 16 lanes of each DPP row; every lane of the row gets the row sum.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp<0x124>(v);  // row_ror:4
+  v += dpp<0x128>(v);  // row_ror:8
+  return v;
+}
+// Sum over the wavefront, result uniform in every lane.
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row16_sum(v);
+  float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (a + b) + (c + d);
+}
+__device__ __forceinline__ float wave_max(float v) {
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+// Block-wide sum (GL3_BLOCK threads); red must hold GL3_WAVES_PER_BLOCK floats.
+__device__ __forceinline__ float block_sum(float v, float *red) {
+  v = wave_sum(v);
+  const int wave = threadIdx.x / GL3_WAVE, lane = threadIdx.x % GL3_WAVE;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float s = 0.0f;
+#pragma unroll
+  for (int w = 0; w < GL3_WAVES_PER_BLOCK; ++w) s += red[w];
+  return s;
+}
+
+// ------------------------------------------------------------ grid barrier
+// Fence-free barrier for the persistent kernel (all workgroups co-resident,
+// guaranteed by the cooperative launch).  Workgroup b arrives on counter
+// b % 8 with a no-return atomic; wave 0 then polls the eight counters in
+// parallel.  Counters only grow: the barrier with global index e (across all
+// launches since the last reset) completes when counter j reaches
+// e * size_of_group(j).  Each poll is bounded: after spin_limit polls the
+// barrier raises *err and every workgroup leaves the kernel at its next
+// barrier, so a lost workgroup can never hang the GPU.
+struct GridBarrier {
+  unsigned *ctr;     // 8 counters, 64 words apart
+  unsigned *err;     // error flag (0 = ok)
+  unsigned spin_limit;
+};
+
+#define GL3_BAR_STRIDE 64
+
+__device__ __forceinline__ bool grid_barrier(const GridBarrier &gb, unsigned epoch) {
+  vmem_drain();
+  __syncthreads();
+  const unsigned nb = gridDim.x;
+  if (threadIdx.x == 0)
+    __hip_atomic_fetch_add(gb.ctr + (blockIdx.x & 7u) * GL3_BAR_STRIDE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __shared__ int bar_ok;
+  if (threadIdx.x < GL3_WAVE) {
+    const unsigned g = threadIdx.x & 7u;
+    const unsigned gsize = nb / 8 + (g < (nb & 7u) ? 1u : 0u);
+    const unsigned target = epoch * gsize;
+    unsigned spins = 0;
+    bool ok = true;
+    for (;;) {
+      unsigned v = (threadIdx.x < 8) ? ld_coherent_u32(gb.ctr + g * GL3_BAR_STRIDE) : target;
+      if (__all((int)(v - target) >= 0)) break;
+      if (ld_coherent_u32(gb.err) != 0u || ++spins > gb.spin_limit) {
+        if (threadIdx.x == 0) st_coherent_u32(gb.err, 1u);
+        ok = false;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (threadIdx.x == 0) bar_ok = ok ? 1 : 0;
+  }
+  __syncthreads();
+  return bar_ok != 0;
+}
+
+}  // namespace gl3

@@ -1,0 +1,35 @@
+// Internal interface between the host plan (gl3_plan.hip) and the kernels
+// (gl3_kernels.hip).
+#pragma once
+
+#include "gl3_phases.h"
+
+namespace gl3 {
+
+struct StepKernel {
+  const void *fn = nullptr;
+  size_t lds_bytes = 0;
+  int barriers_per_step = 0;
+};
+
+int gemv_n(int fmt, int K);
+bool gemv_supported(int fmt, int K);
+hipError_t launch_gemv(int fmt, int mode, const Mat &W, int out_rows, const float *x, const float *normw, float eps,
+                       float *y, unsigned long long *best, int grid, hipStream_t s);
+hipError_t launch_logits(const ModelDev &m, int grid, hipStream_t s);
+size_t attention_lds_bytes(int hd, int G);
+hipError_t launch_embed(const ModelDev &m, hipStream_t s);
+hipError_t launch_attention(const ModelDev &m, int layer, hipStream_t s);
+hipError_t launch_advance(const ModelDev &m, hipStream_t s);
+hipError_t launch_finish(const ModelDev &m, hipStream_t s);
+
+bool find_step_kernel(const ModelDev &m, StepKernel *out);
+hipError_t launch_step_kernel(const StepKernel &k, const ModelDev &m, const GridBarrier &gb, unsigned epoch, int grid,
+                              hipStream_t s);
+
+hipError_t launch_repack_q8(const uint8_t *blocks, size_t nblocks, uint8_t *q, uint16_t *s, hipStream_t st);
+hipError_t launch_dequant_q8(const uint8_t *q, const uint16_t *s, size_t n, float *out, hipStream_t st);
+hipError_t launch_f16_to_f32(const uint16_t *in, size_t n, float *out, hipStream_t st);
+hipError_t launch_fill_normal_f16(uint16_t *dst, size_t n, unsigned long long seed, hipStream_t st);
+
+}  // namespace gl3

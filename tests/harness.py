@@ -1,0 +1,44 @@
+"""Shared helpers: build the device plan and the oracle from the same tensors."""
+import numpy as np
+
+import oracle.oracle as orc
+from gpullama3_hip import HipMasterPlan
+from gpullama3_hip.model import CONFIGS, synth_model
+
+# Per-layer shapes of the five workloads (with few layers and a small vocabulary
+# they keep the compile-time GEMV shapes of the persistent kernel).
+LAYER_SHAPES = {
+    "llama1b_q8": CONFIGS["llama1b_q8"],
+    "llama1b_f16": CONFIGS["llama1b_f16"],
+    "qwen3_06b_q8": CONFIGS["qwen3_06b_q8"],
+    "phi3_mini_f16": CONFIGS["phi3_mini_f16"],
+    "llama8b_q8": CONFIGS["llama8b_q8"],
+}
+
+
+def small(key, n_layers=2, vocab=4096, ctx=512):
+    return LAYER_SHAPES[key].with_(n_layers=n_layers, vocab_size=vocab, context_length=ctx)
+
+
+def build(shape, seed=7, flags=0, norm_init="random", kv_fp16=True, threads=0):
+    tensors = synth_model(shape, seed, norm_init=norm_init)
+    plan = HipMasterPlan.initialize_plan(shape, tensors, flags=flags)
+    ref = orc.OracleModel(shape, tensors, kv_fp16=kv_fp16, n_threads=threads)
+    return plan, ref, tensors
+
+
+def prefill_kv(plan, ref, shape, npos, seed=3):
+    """Same fp16 N(0,1) history in both caches for positions [0, npos)."""
+    rng = np.random.default_rng(seed)
+    for l in range(shape.n_layers):
+        k = rng.standard_normal((npos, shape.kv_dim), dtype=np.float32).astype(np.float16)
+        v = rng.standard_normal((npos, shape.kv_dim), dtype=np.float32).astype(np.float16)
+        plan.write_kv(l, 0, k.view(np.uint16), v.view(np.uint16))
+        rk, rv = ref.kv(l)
+        rk[:npos] = k.astype(np.float32)
+        rv[:npos] = v.astype(np.float32)
+
+
+def top2_margin(logits):
+    s = np.sort(logits)
+    return float(s[-1] - s[-2])
