@@ -7,8 +7,8 @@
 #include <stdint.h>
 
 #define GL3_WAVE 64
-#define GL3_BLOCK 256
-#define GL3_WAVES_PER_BLOCK (GL3_BLOCK / GL3_WAVE)
+#define GL3_BLOCK 256         // threads per workgroup of the per-phase kernels
+#define GL3_STEP_BLOCK 256    // threads per workgroup of the persistent per-token kernel and attention
 
 namespace gl3 {
 
@@ -51,6 +51,18 @@ __device__ __forceinline__ int ld_coherent_i32(const int *p) {
 __device__ __forceinline__ unsigned long long ld_coherent_u64(const unsigned long long *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// 16-byte coherent load (buffer_load_dwordx4 with the agent-scope sc1 bit).
+// Unlike the atomic loads above, the compiler may batch these, so a loop of
+// them keeps many requests in flight.  Out-of-range offsets read zeros.
+__device__ __forceinline__ u32x4 ld_coherent_x4(const void *base, unsigned byte_off) {
+  __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, 0x7fffffff, 0x00020000);
+  return __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 16 /* sc1 */);
+}
+__device__ __forceinline__ float4 ld_coherent_f4(const float *base, unsigned index) {
+  u32x4 v = ld_coherent_x4(base, index * 4u);
+  return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+}
+
 // Wait until this wave's outstanding vector-memory operations (including the
 // coherent stores above) have completed.  Used instead of a release fence
 // before signalling another workgroup.
@@ -88,7 +100,9 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
-// Block-wide sum (GL3_BLOCK threads); red must hold GL3_WAVES_PER_BLOCK floats.
+// Block-wide sum over BS threads; red must hold BS/64 floats.  Ends with the
+// result visible to every thread; red may be reused after the call.
+template <int BS>
 __device__ __forceinline__ float block_sum(float v, float *red) {
   v = wave_sum(v);
   const int wave = threadIdx.x / GL3_WAVE, lane = threadIdx.x % GL3_WAVE;
@@ -97,8 +111,20 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
   __syncthreads();
   float s = 0.0f;
 #pragma unroll
-  for (int w = 0; w < GL3_WAVES_PER_BLOCK; ++w) s += red[w];
+  for (int w = 0; w < BS / GL3_WAVE; ++w) s += red[w];
   return s;
+}
+
+// Sum over aligned groups of LP lanes (LP = 8 or 16); every lane of a group
+// gets the group's sum.  quad_perm xor 1, xor 2, then row_half_mirror (the
+// other quad of the 8-lane half row) and, for 16, row_mirror (the other half).
+template <int LP>
+__device__ __forceinline__ float group_sum(float v) {
+  v += dpp<0xB1>(v);
+  v += dpp<0x4E>(v);
+  v += dpp<0x141>(v);
+  if (LP == 16) v += dpp<0x140>(v);
+  return v;
 }
 
 // ------------------------------------------------------------ grid barrier
@@ -118,12 +144,20 @@ struct GridBarrier {
 
 #define GL3_BAR_STRIDE 64
 
-__device__ __forceinline__ bool grid_barrier(const GridBarrier &gb, unsigned epoch) {
+// Arrival: this workgroup's earlier writes are complete, then one no-return
+// atomic on its group counter.  Loads issued between grid_arrive and grid_wait
+// (e.g. weights of the next phase) overlap the wait.
+__device__ __forceinline__ void grid_arrive(const GridBarrier &gb) {
   vmem_drain();
   __syncthreads();
-  const unsigned nb = gridDim.x;
   if (threadIdx.x == 0)
     __hip_atomic_fetch_add(gb.ctr + (blockIdx.x & 7u) * GL3_BAR_STRIDE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Waits until every workgroup has arrived at barrier `epoch`; false when the
+// barrier timed out or another workgroup raised the error flag.
+__device__ __forceinline__ bool grid_wait(const GridBarrier &gb, unsigned epoch) {
+  const unsigned nb = gridDim.x;
   __shared__ int bar_ok;
   if (threadIdx.x < GL3_WAVE) {
     const unsigned g = threadIdx.x & 7u;
@@ -145,6 +179,11 @@ __device__ __forceinline__ bool grid_barrier(const GridBarrier &gb, unsigned epo
   }
   __syncthreads();
   return bar_ok != 0;
+}
+
+__device__ __forceinline__ bool grid_barrier(const GridBarrier &gb, unsigned epoch) {
+  grid_arrive(gb);
+  return grid_wait(gb, epoch);
 }
 
 }  // namespace gl3

@@ -17,13 +17,14 @@ bool gemv_supported(int fmt, int K);
 hipError_t launch_gemv(int fmt, int mode, const Mat &W, int out_rows, const float *x, const float *normw, float eps,
                        float *y, unsigned long long *best, int grid, hipStream_t s);
 hipError_t launch_logits(const ModelDev &m, int grid, hipStream_t s);
-size_t attention_lds_bytes(int hd, int G);
+size_t attention_lds_bytes(int hd, int G, int max_split);
+bool attention_supported(int hd, int G);
 hipError_t launch_embed(const ModelDev &m, hipStream_t s);
 hipError_t launch_attention(const ModelDev &m, int layer, hipStream_t s);
 hipError_t launch_advance(const ModelDev &m, hipStream_t s);
 hipError_t launch_finish(const ModelDev &m, hipStream_t s);
 
-bool find_step_kernel(const ModelDev &m, StepKernel *out);
+bool find_step_kernel(const ModelDev &m, int grid, StepKernel *out);
 hipError_t launch_step_kernel(const StepKernel &k, const ModelDev &m, const GridBarrier &gb, unsigned epoch, int grid,
                               hipStream_t s);
 

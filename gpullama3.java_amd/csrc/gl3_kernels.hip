@@ -20,9 +20,10 @@ namespace gl3 {
   X(FMT_F16, 2, 2, 1) X(FMT_F16, 4, 4, 1) X(FMT_F16, 6, 6, 1)  \
   X(FMT_F16, 8, 8, 1) X(FMT_F16, 16, 8, 2) X(FMT_F16, 28, 7, 4)
 
+// Rows per wave for the per-phase kernels: small tiles, many resident waves.
 template <int KC, int NP>
 struct DefaultNR {
-  static constexpr int v = (8 / (KC * NP)) > 0 ? (8 / (KC * NP)) : 1;
+  static constexpr int v = (4 / (KC * NP)) > 0 ? (4 / (KC * NP)) : 1;
 };
 
 template <class P>
@@ -35,9 +36,9 @@ __global__ __launch_bounds__(GL3_BLOCK) void gemv_kernel(Mat W, int out_rows, co
 template <class P>
 static hipError_t launch_gemv_t(const Mat &W, int out_rows, const float *x, const float *normw, float eps, float *y,
                                 unsigned long long *best, int grid, hipStream_t s) {
-  const int items = (out_rows + P::ROWS_PER_ITEM - 1) / P::ROWS_PER_ITEM;
-  if (grid <= 0) grid = items < 2048 ? items : 2048;
-  size_t lds = P::lds_bytes(W.cols);
+  const int items = P::items(out_rows);
+  if (grid <= 0) grid = items < 8192 ? items : 8192;
+  size_t lds = P::lds_bytes(W.cols, out_rows, grid, normw != nullptr);
   hipLaunchKernelGGL(gemv_kernel<P>, dim3(grid), dim3(GL3_BLOCK), lds, s, W, out_rows, x, normw, eps, y, best);
   return hipGetLastError();
 }
@@ -62,16 +63,16 @@ hipError_t launch_gemv(int fmt, int mode, const Mat &W, int out_rows, const floa
   if (fmt == F && n == N) {                                                                                         \
     switch (mode) {                                                                                                 \
       case MODE_STORE:                                                                                              \
-        return launch_gemv_t<GemvPhase<F, KC, KS, DefaultNR<KC, 1>::v, MODE_STORE>>(W, out_rows, x, normw, eps, y,  \
+        return launch_gemv_t<GemvPhase<F, KC, KS, DefaultNR<KC, 1>::v, MODE_STORE, GL3_BLOCK>>(W, out_rows, x, normw, eps, y,  \
                                                                                     best, grid, s);                 \
       case MODE_RESIDUAL:                                                                                           \
-        return launch_gemv_t<GemvPhase<F, KC, KS, DefaultNR<KC, 1>::v, MODE_RESIDUAL>>(W, out_rows, x, normw, eps, \
+        return launch_gemv_t<GemvPhase<F, KC, KS, DefaultNR<KC, 1>::v, MODE_RESIDUAL, GL3_BLOCK>>(W, out_rows, x, normw, eps, \
                                                                                        y, best, grid, s);           \
       case MODE_SWIGLU:                                                                                             \
-        return launch_gemv_t<GemvPhase<F, KC, KS, DefaultNR<KC, 2>::v, MODE_SWIGLU>>(W, out_rows, x, normw, eps, y, \
+        return launch_gemv_t<GemvPhase<F, KC, KS, DefaultNR<KC, 2>::v, MODE_SWIGLU, GL3_BLOCK>>(W, out_rows, x, normw, eps, y, \
                                                                                      best, grid, s);                \
       default:                                                                                                      \
-        return launch_gemv_t<GemvPhase<F, KC, KS, DefaultNR<KC, 1>::v, MODE_LOGITS>>(W, out_rows, x, normw, eps, y, \
+        return launch_gemv_t<GemvPhase<F, KC, KS, DefaultNR<KC, 1>::v, MODE_LOGITS, GL3_BLOCK>>(W, out_rows, x, normw, eps, y, \
                                                                                      best, grid, s);                \
     }                                                                                                               \
   }
@@ -93,8 +94,8 @@ hipError_t launch_logits(const ModelDev &m, int grid, hipStream_t s) {
   const int n = gemv_n(m.cls_fmt, m.dim);
 #define GL3_LOGITS(F, N, KC, KS)                                                                     \
   if (m.cls_fmt == F && n == N) {                                                                    \
-    typedef GemvPhase<F, KC, KS, DefaultNR<KC, 1>::v, MODE_LOGITS> P;                                \
-    hipLaunchKernelGGL(logits_kernel<P>, dim3(grid), dim3(GL3_BLOCK), P::lds_bytes(m.dim), s, m);    \
+    typedef GemvPhase<F, KC, KS, DefaultNR<KC, 1>::v, MODE_LOGITS, GL3_BLOCK> P;                                \
+    hipLaunchKernelGGL(logits_kernel<P>, dim3(grid), dim3(GL3_BLOCK), P::lds_bytes(m.dim, m.vocab, grid, true), s, m); \
     return hipGetLastError();                                                                        \
   }
   GL3_GEMV_LIST(GL3_LOGITS)
@@ -110,11 +111,12 @@ __global__ __launch_bounds__(GL3_BLOCK) void embed_kernel(ModelDev m) {
   phase_embed(m, si.token, blockIdx.x, gridDim.x);
 }
 
-__global__ __launch_bounds__(GL3_BLOCK) void attention_kernel(ModelDev m, int layer) {
+template <int LP, int GQ>
+__global__ __launch_bounds__(GL3_STEP_BLOCK) void attention_kernel(ModelDev m, int layer) {
   extern __shared__ float lds[];
   __shared__ int si_lds[8];
   StepInfo si = read_step(m, si_lds);
-  phase_attention(m, layer, si.pos, blockIdx.x, gridDim.x, lds);
+  phase_attention<LP, GQ, GL3_STEP_BLOCK>(m, layer, si.pos, blockIdx.x, gridDim.x, lds);
 }
 
 // Last kernel of a step: records the previous token and advances the control block.
@@ -131,10 +133,12 @@ __global__ __launch_bounds__(GL3_BLOCK) void finish_kernel(ModelDev m) {
   if (threadIdx.x == 0 && si.from_best && si.step > 0) m.tokens_out[si.step - 1] = si.token;
 }
 
-size_t attention_lds_bytes(int hd, int G) {
-  return ((size_t)G * hd + 2 * hd + ATT_TILE * (hd + 1) + ATT_TILE * hd + G * ATT_TILE + 3 * ATT_MAX_G + 16 + 8 + 16) *
-         sizeof(float);
+size_t attention_lds_bytes(int hd, int G, int max_split) {
+  return (size_t)att_lds_floats(hd, G, GL3_STEP_BLOCK / GL3_WAVE, max_split) * sizeof(float);
 }
+
+// lanes per KV position: 8 for head_dim <= 64, 16 for head_dim <= 128
+static int att_lp(int hd) { return hd <= 64 ? 8 : 16; }
 
 hipError_t launch_embed(const ModelDev &m, hipStream_t s) {
   int grid = (m.dim + GL3_BLOCK - 1) / GL3_BLOCK;
@@ -143,10 +147,19 @@ hipError_t launch_embed(const ModelDev &m, hipStream_t s) {
 }
 hipError_t launch_attention(const ModelDev &m, int layer, hipStream_t s) {
   const int grid = m.n_kv * m.max_split;
-  hipLaunchKernelGGL(attention_kernel, dim3(grid), dim3(GL3_BLOCK), attention_lds_bytes(m.hd, m.n_heads / m.n_kv), s,
-                     m, layer);
-  return hipGetLastError();
+  const int G = m.n_heads / m.n_kv, lp = att_lp(m.hd);
+  const size_t lds = attention_lds_bytes(m.hd, G, m.max_split);
+#define GL3_ATT(LP_, G_)                                                                                        \
+  if (lp == LP_ && G == G_) {                                                                                   \
+    hipLaunchKernelGGL((attention_kernel<LP_, G_>), dim3(grid), dim3(GL3_STEP_BLOCK), lds, s, m, layer);        \
+    return hipGetLastError();                                                                                   \
+  }
+  GL3_ATT(8, 1) GL3_ATT(8, 2) GL3_ATT(8, 4) GL3_ATT(8, 8)
+  GL3_ATT(16, 1) GL3_ATT(16, 2) GL3_ATT(16, 4) GL3_ATT(16, 8)
+#undef GL3_ATT
+  return hipErrorInvalidValue;
 }
+bool attention_supported(int hd, int G) { return hd % 8 == 0 && hd <= 128 && (G == 1 || G == 2 || G == 4 || G == 8) && G * hd <= 4 * GL3_STEP_BLOCK; }
 hipError_t launch_advance(const ModelDev &m, hipStream_t s) {
   hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(GL3_BLOCK), 0, s, m);
   return hipGetLastError();
@@ -158,89 +171,128 @@ hipError_t launch_finish(const ModelDev &m, hipStream_t s) {
 
 // --------------------------------------------------- persistent step kernel
 
-// Compile-time GEMV shapes of the model families the persistent kernel is
-// built for.  NR is chosen so that every phase has >= 256 work items.
-template <int FMT, int CLSF, int DIM, int QD, int KVD, int HID, int NRQKV, int NRWO, int NRGU, int NRDN, int NRCLS>
+// Compile-time shapes of the models the persistent kernel is built for.  Each
+// GEMV phase lists its tile (KC chunks per lane, KS waves splitting K, NR rows
+// per wave) for 4-wave workgroups, chosen so that a wave's tile fills one ring
+// slot of SC chunks and the work items of every phase spread evenly over the
+// CUs.  DEPTH ring slots per wave are in flight.
+template <int KC_, int KS_, int NR_>
+struct Tile {
+  static constexpr int KC = KC_, KS = KS_, NR = NR_;
+};
+template <int FMT_, int DIM, int QD, int KVD, int HID, int HD, int G, int SC, int DEPTH, class TQKV, class TWO,
+          class TGU, class TDN, class TCLS>
 struct Shape {
-  static constexpr int fmt = FMT, cls_fmt = CLSF, dim = DIM, q_dim = QD, kv_dim = KVD, hidden = HID;
-  static constexpr int EPC = FMT == FMT_Q8 ? 16 : 8;
-  static constexpr int CEPC = CLSF == FMT_Q8 ? 16 : 8;
-  static constexpr int nd = DIM / (EPC * 64), nq = QD / (EPC * 64), nh = HID / (EPC * 64), nc = DIM / (CEPC * 64);
-  // split K so that a lane holds at most 64 (Q8: 7*16=112 for n=14) x values
-  static constexpr int ks(int n, int kcmax) { return n <= kcmax ? 1 : (n / 2 <= kcmax ? 2 : 4); }
-  static constexpr int KCMAX = FMT == FMT_Q8 ? 7 : 8;
-  static constexpr int CKCMAX = CLSF == FMT_Q8 ? 7 : 8;
-  typedef GemvPhase<FMT, nd / ks(nd, KCMAX), ks(nd, KCMAX), NRQKV, MODE_STORE> QKV;
-  typedef GemvPhase<FMT, nq / ks(nq, KCMAX), ks(nq, KCMAX), NRWO, MODE_RESIDUAL> WO;
-  typedef GemvPhase<FMT, nd / ks(nd, KCMAX), ks(nd, KCMAX), NRGU, MODE_SWIGLU> GU;
-  typedef GemvPhase<FMT, nh / ks(nh, KCMAX), ks(nh, KCMAX), NRDN, MODE_RESIDUAL> DOWN;
-  typedef GemvPhase<CLSF, nc / ks(nc, CKCMAX), ks(nc, CKCMAX), NRCLS, MODE_LOGITS> CLS;
+  static constexpr int fmt = FMT_, dim = DIM, q_dim = QD, kv_dim = KVD, hidden = HID, hd = HD, gqa = G;
+  static constexpr int BS = GL3_STEP_BLOCK;
+  static constexpr int LP = HD <= 64 ? 8 : 16;
+  typedef GemvPhase<FMT_, TQKV::KC, TQKV::KS, TQKV::NR, MODE_STORE, BS, SC, DEPTH> QKV;
+  typedef GemvPhase<FMT_, TWO::KC, TWO::KS, TWO::NR, MODE_RESIDUAL, BS, SC, DEPTH> WO;
+  typedef GemvPhase<FMT_, TGU::KC, TGU::KS, TGU::NR, MODE_SWIGLU, BS, SC, DEPTH> GU;
+  typedef GemvPhase<FMT_, TDN::KC, TDN::KS, TDN::NR, MODE_RESIDUAL, BS, SC, DEPTH> DOWN;
+  typedef GemvPhase<FMT_, TCLS::KC, TCLS::KS, TCLS::NR, MODE_LOGITS, BS, SC, DEPTH> CLS;
 };
 
-// Llama-3.2-1B (Q8_0 and F16), Qwen3-0.6B (Q8_0), Phi-3-mini (F16), Llama-3.1-8B (Q8_0)
-typedef Shape<FMT_Q8, FMT_Q8, 2048, 2048, 512, 8192, 3, 2, 4, 2, 4> ShapeLlama1BQ8;
-typedef Shape<FMT_F16, FMT_F16, 2048, 2048, 512, 8192, 2, 2, 2, 2, 2> ShapeLlama1BF16;
-typedef Shape<FMT_Q8, FMT_Q8, 1024, 2048, 1024, 3072, 4, 1, 3, 1, 4> ShapeQwen3_06BQ8;
-typedef Shape<FMT_F16, FMT_F16, 3072, 3072, 3072, 8192, 2, 2, 1, 2, 2> ShapePhi3MiniF16;
-typedef Shape<FMT_Q8, FMT_Q8, 4096, 4096, 1024, 14336, 2, 2, 1, 1, 2> ShapeLlama8BQ8;
+//                  fmt     dim   q_dim kv_dim hidden hd  G SC D  QKV           WO            GU            DOWN          CLS
+typedef Shape<FMT_Q8,  2048, 2048,  512,  8192,  64, 4, 8, 3, Tile<2, 1, 3>, Tile<2, 1, 2>, Tile<2, 1, 2>, Tile<2, 4, 4>, Tile<2, 1, 4>> ShapeLlama1BQ8;
+typedef Shape<FMT_F16, 2048, 2048,  512,  8192,  64, 4, 8, 3, Tile<4, 1, 3>, Tile<4, 1, 2>, Tile<4, 1, 1>, Tile<4, 4, 2>, Tile<4, 1, 2>> ShapeLlama1BF16;
+typedef Shape<FMT_Q8,  1024, 2048, 1024,  3072, 128, 2, 8, 3, Tile<1, 1, 4>, Tile<1, 2, 2>, Tile<1, 1, 3>, Tile<3, 1, 1>, Tile<1, 1, 8>> ShapeQwen3_06BQ8;
+typedef Shape<FMT_F16, 3072, 3072, 3072,  8192,  96, 1, 8, 3, Tile<6, 1, 1>, Tile<6, 1, 1>, Tile<3, 2, 1>, Tile<4, 4, 2>, Tile<6, 1, 1>> ShapePhi3MiniF16;
+typedef Shape<FMT_Q8,  4096, 4096, 1024, 14336, 128, 4, 8, 3, Tile<4, 1, 2>, Tile<4, 1, 2>, Tile<4, 1, 1>, Tile<7, 2, 1>, Tile<4, 1, 2>> ShapeLlama8BQ8;
 
+// One decode step in one launch: embedding, L x (QKV, attention, Wo, gate/up,
+// down), classifier, with a grid barrier between dependent phases.  The first
+// weight tiles of each GEMV phase are requested before the barrier that
+// precedes it (weights do not depend on it), so their HBM latency overlaps
+// the barrier and, for Wo, the attention phase.
 template <class SH>
-__global__ __launch_bounds__(GL3_BLOCK, 1) void decode_step_kernel(ModelDev m, GridBarrier gb, unsigned epoch) {
+__global__ __launch_bounds__(GL3_STEP_BLOCK, 1) void decode_step_kernel(ModelDev m, GridBarrier gb, unsigned epoch) {
   extern __shared__ float lds[];
   __shared__ int si_lds[8];
   const int blk = blockIdx.x, nblk = gridDim.x;
+  const int rows_qkv = SH::q_dim + 2 * SH::kv_dim;
+  int tk = 0;
+  trace(m, tk++);
   StepInfo si = read_step(m, si_lds);
   phase_embed(m, si.token, blk, nblk);
-  if (!grid_barrier(gb, ++epoch)) return;
+  trace(m, tk++);
+  grid_arrive(gb);
+  SH::QKV::prefetch(m.layers[0].qkv, rows_qkv, blk, nblk);
+  if (!grid_wait(gb, ++epoch)) return;
+  trace(m, tk++);
   if (blk == 0) advance_step(m, si);
-  const int rows_qkv = SH::q_dim + 2 * SH::kv_dim;
   for (int l = 0; l < m.n_layers; ++l) {
     const LayerDev &L = m.layers[l];
-    SH::QKV::run(L.qkv, rows_qkv, m.x, L.attn_norm, m.eps, m.qkv, nullptr, blk, nblk, lds);
+    SH::QKV::run(L.qkv, rows_qkv, m.x, L.attn_norm, m.eps, m.qkv, nullptr, blk, nblk, lds, true);
+    trace(m, tk++);
+    grid_arrive(gb);
+    SH::WO::prefetch(L.wo, SH::dim, blk, nblk);
+    if (!grid_wait(gb, ++epoch)) return;
+    trace(m, tk++);
+    phase_attention<SH::LP, SH::gqa, SH::BS>(m, l, si.pos, blk, nblk, lds);
+    trace(m, tk++);
     if (!grid_barrier(gb, ++epoch)) return;
-    phase_attention(m, l, si.pos, blk, nblk, lds);
-    if (!grid_barrier(gb, ++epoch)) return;
-    SH::WO::run(L.wo, SH::dim, m.att, nullptr, m.eps, m.x, nullptr, blk, nblk, lds);
-    if (!grid_barrier(gb, ++epoch)) return;
-    SH::GU::run(L.gu, SH::hidden, m.x, L.ffn_norm, m.eps, m.hb, nullptr, blk, nblk, lds);
-    if (!grid_barrier(gb, ++epoch)) return;
-    SH::DOWN::run(L.down, SH::dim, m.hb, nullptr, m.eps, m.x, nullptr, blk, nblk, lds);
-    if (!grid_barrier(gb, ++epoch)) return;
+    trace(m, tk++);
+    SH::WO::run(L.wo, SH::dim, m.att, nullptr, m.eps, m.x, nullptr, blk, nblk, lds, true);
+    trace(m, tk++);
+    grid_arrive(gb);
+    SH::GU::prefetch(L.gu, SH::hidden, blk, nblk);
+    if (!grid_wait(gb, ++epoch)) return;
+    trace(m, tk++);
+    SH::GU::run(L.gu, SH::hidden, m.x, L.ffn_norm, m.eps, m.hb, nullptr, blk, nblk, lds, true);
+    trace(m, tk++);
+    grid_arrive(gb);
+    SH::DOWN::prefetch(L.down, SH::dim, blk, nblk);
+    if (!grid_wait(gb, ++epoch)) return;
+    trace(m, tk++);
+    SH::DOWN::run(L.down, SH::dim, m.hb, nullptr, m.eps, m.x, nullptr, blk, nblk, lds, true);
+    trace(m, tk++);
+    grid_arrive(gb);
+    if (l + 1 < m.n_layers)
+      SH::QKV::prefetch(m.layers[l + 1].qkv, rows_qkv, blk, nblk);
+    else
+      SH::CLS::prefetch(m.cls, m.vocab, blk, nblk);
+    if (!grid_wait(gb, ++epoch)) return;
+    trace(m, tk++);
   }
   SH::CLS::run(m.cls, m.vocab, m.x, m.out_norm, m.eps, m.logits, m.best + (size_t)si.parity * si.nbest, blk, nblk,
-               lds);
+               lds, true);
+  trace(m, tk++);
 }
 
 template <class SH>
 static bool shape_matches(const ModelDev &m) {
-  return m.fmt == SH::fmt && m.cls_fmt == SH::cls_fmt && m.dim == SH::dim && m.q_dim == SH::q_dim &&
-         m.kv_dim == SH::kv_dim && m.hidden == SH::hidden;
+  return m.fmt == SH::fmt && m.cls_fmt == SH::fmt && m.dim == SH::dim && m.q_dim == SH::q_dim &&
+         m.kv_dim == SH::kv_dim && m.hidden == SH::hidden && m.hd == SH::hd && m.n_heads / m.n_kv == SH::gqa;
 }
 
 template <class SH>
-static size_t step_lds_bytes(const ModelDev &m) {
-  size_t b = attention_lds_bytes(m.hd, m.n_heads / m.n_kv);
-  size_t g[5] = {SH::QKV::lds_bytes(SH::dim), SH::WO::lds_bytes(SH::q_dim), SH::GU::lds_bytes(SH::dim),
-                 SH::DOWN::lds_bytes(SH::hidden), SH::CLS::lds_bytes(SH::dim)};
+static size_t step_lds_bytes(const ModelDev &m, int grid) {
+  size_t b = attention_lds_bytes(m.hd, m.n_heads / m.n_kv, m.max_split);
+  const int rows_qkv = SH::q_dim + 2 * SH::kv_dim;
+  size_t g[5] = {SH::QKV::lds_bytes(SH::dim, rows_qkv, grid, true), SH::WO::lds_bytes(SH::q_dim, SH::dim, grid, false),
+                 SH::GU::lds_bytes(SH::dim, SH::hidden, grid, true),
+                 SH::DOWN::lds_bytes(SH::hidden, SH::dim, grid, false),
+                 SH::CLS::lds_bytes(SH::dim, m.vocab, grid, true)};
   for (size_t v : g) b = v > b ? v : b;
   return b;
 }
 
 template <class SH>
-static StepKernel make_step_kernel(const ModelDev &m) {
+static StepKernel make_step_kernel(const ModelDev &m, int grid) {
   StepKernel k;
   k.fn = (const void *)decode_step_kernel<SH>;
-  k.lds_bytes = step_lds_bytes<SH>(m);
+  k.lds_bytes = step_lds_bytes<SH>(m, grid);
   k.barriers_per_step = 1 + 5 * m.n_layers;
   return k;
 }
 
-bool find_step_kernel(const ModelDev &m, StepKernel *out) {
-  if (shape_matches<ShapeLlama1BQ8>(m)) { *out = make_step_kernel<ShapeLlama1BQ8>(m); return true; }
-  if (shape_matches<ShapeLlama1BF16>(m)) { *out = make_step_kernel<ShapeLlama1BF16>(m); return true; }
-  if (shape_matches<ShapeQwen3_06BQ8>(m)) { *out = make_step_kernel<ShapeQwen3_06BQ8>(m); return true; }
-  if (shape_matches<ShapePhi3MiniF16>(m)) { *out = make_step_kernel<ShapePhi3MiniF16>(m); return true; }
-  if (shape_matches<ShapeLlama8BQ8>(m)) { *out = make_step_kernel<ShapeLlama8BQ8>(m); return true; }
+bool find_step_kernel(const ModelDev &m, int grid, StepKernel *out) {
+  if (shape_matches<ShapeLlama1BQ8>(m)) { *out = make_step_kernel<ShapeLlama1BQ8>(m, grid); return true; }
+  if (shape_matches<ShapeLlama1BF16>(m)) { *out = make_step_kernel<ShapeLlama1BF16>(m, grid); return true; }
+  if (shape_matches<ShapeQwen3_06BQ8>(m)) { *out = make_step_kernel<ShapeQwen3_06BQ8>(m, grid); return true; }
+  if (shape_matches<ShapePhi3MiniF16>(m)) { *out = make_step_kernel<ShapePhi3MiniF16>(m, grid); return true; }
+  if (shape_matches<ShapeLlama8BQ8>(m)) { *out = make_step_kernel<ShapeLlama8BQ8>(m, grid); return true; }
   return false;
 }
 
@@ -250,7 +302,7 @@ hipError_t launch_step_kernel(const StepKernel &k, const ModelDev &m, const Grid
   GridBarrier gg = gb;
   unsigned e = epoch;
   void *args[] = {&mm, &gg, &e};
-  return hipLaunchCooperativeKernel(k.fn, dim3(grid), dim3(GL3_BLOCK), args, (unsigned)k.lds_bytes, s);
+  return hipLaunchCooperativeKernel(k.fn, dim3(grid), dim3(GL3_STEP_BLOCK), args, (unsigned)k.lds_bytes, s);
 }
 
 // -------------------------------------------------------------- op kernels

@@ -1,8 +1,8 @@
 // The phases of one decode step, written once and used by both schedules:
 // the per-phase kernels (one launch per phase, captured in a hipGraph) and the
 // persistent per-token kernel (all phases in one launch, separated by grid
-// barriers).  Every phase is a grid-stride loop over its work items, so it runs
-// on any number of workgroups of GL3_BLOCK threads.
+// barriers).  Every phase is a grid-stride loop over its work items and is
+// templated on the workgroup size BS, so it runs on any number of workgroups.
 //
 // Reference paths are relative to src/main/java/org/beehive/gpullama3/.
 #pragma once
@@ -61,12 +61,20 @@ struct ModelDev {
   float *att;               // attention output [q_dim]
   float *hb;                // SwiGLU output [hidden]
   float *logits;            // [vocab]
-  float *part;              // attention partials [n_heads][max_split][hd + 2]
+  float *part;              // attention partials [n_heads][max_split][hd + 4]: o[hd], m, l, pad
   unsigned *att_ctr;        // split-merge counters [L][n_kv]
   unsigned long long *best; // argmax keys [2][nbest]
   DecodeState *st;
   int *tokens_out;          // device copy of generated tokens
+  unsigned long long *tstamp;  // optional phase trace: s_memrealtime at each phase boundary (workgroup 0)
 };
+
+// Phase trace of the persistent kernel: workgroup 0 stamps the 100 MHz real-time
+// counter when it leaves a phase (before the grid barrier) and when it enters
+// the next one (after the barrier).
+__device__ __forceinline__ void trace(const ModelDev &m, int idx) {
+  if (m.tstamp && blockIdx.x == 0 && threadIdx.x == 0) m.tstamp[idx] = __builtin_amdgcn_s_memrealtime();
+}
 
 // ------------------------------------------------------------ step control
 
@@ -136,7 +144,7 @@ __device__ inline void advance_step(const ModelDev &m, const StepInfo &si) {
 // the fp32-converted row on the host, InferenceCore.java:586).
 __device__ inline void phase_embed(const ModelDev &m, int token, int blk, int nblk) {
   const int dim = m.dim;
-  for (int i = blk * GL3_BLOCK + threadIdx.x; i < dim; i += nblk * GL3_BLOCK) {
+  for (int i = blk * blockDim.x + threadIdx.x; i < dim; i += nblk * blockDim.x) {
     size_t e = (size_t)token * dim + i;
     float v;
     if (m.embd_fmt == FMT_F32) {
@@ -156,8 +164,10 @@ __device__ inline void phase_embed(const ModelDev &m, int token, int blk, int nb
 // chunks of every row, so its slice of x stays in registers for all rows.
 // Weights stream with 128-bit non-temporal loads, are converted in registers
 // (Q8_0: one sign-extending byte->float conversion per element, per 16-element
-// chunk acc += s * sum(q*x); F16: exact half->float), and accumulate in fp32.  No MFMA: batch-1 GEMV is
-// bound by HBM bandwidth.
+// chunk acc += s * sum(q*x); F16: exact half->float), and accumulate in fp32.
+// No MFMA: batch-1 GEMV is bound by HBM bandwidth.  Latency is hidden by many
+// resident waves; the first tile of a workgroup can be loaded before the grid
+// barrier that precedes the phase (it does not depend on the previous phase).
 //
 // Follows matrixVectorGeneric / matrixVectorGenericWithResidual /
 // fusedFeedForwardWithSiLUAndGLUActivation (kernels/TransformerComputeKernelsLayered.java:650-1057).
@@ -177,91 +187,252 @@ struct ChunkTraits<FMT_F16> {
 
 // Load x (coherently) into LDS, applying RMSNorm when normw != nullptr:
 // xs[i] = normw[i] * (ss * x[i]), ss = 1/sqrt(mean(x^2) + eps) (InferenceCore.java:46-55).
+// K must be a multiple of 4.
+template <int BS>
 __device__ inline void load_x_lds(const float *x, const float *normw, float eps, int K, float *xs, float *red) {
-  float ss = 0.0f;
-  for (int i = threadIdx.x; i < K; i += GL3_BLOCK) {
-    float v = ld_coherent(x + i);
-    xs[i] = v;
-    ss += v * v;
+  if (!normw) {
+#pragma unroll 4
+    for (int i = 4 * threadIdx.x; i < K; i += 4 * BS) *(float4 *)(xs + i) = ld_coherent_f4(x, i);
+    __syncthreads();
+    return;
   }
-  if (normw) {
-    ss = block_sum(ss, red);
+  if (K > 16 * BS) {  // wide vectors: weights read after the reduction
+    float ss = 0.0f;
+    for (int i = 4 * threadIdx.x; i < K; i += 4 * BS) {
+      float4 v = ld_coherent_f4(x, i);
+      *(float4 *)(xs + i) = v;
+      ss += v.x * v.x;
+      ss += v.y * v.y;
+      ss += v.z * v.z;
+      ss += v.w * v.w;
+    }
+    ss = block_sum<BS>(ss, red);
     ss /= (float)K;
     ss += eps;
     ss = (float)(1.0 / sqrt((double)ss));
-    for (int i = threadIdx.x; i < K; i += GL3_BLOCK) xs[i] = normw[i] * (ss * xs[i]);
+    for (int i = threadIdx.x; i < K; i += BS) xs[i] = normw[i] * (ss * xs[i]);
+    __syncthreads();
+    return;
+  }
+  // x and the norm weights are fetched together; the weights wait in registers
+  // (up to 4 float4 per thread) while the sum of squares is reduced.
+  float ss = 0.0f;
+  float4 wv[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int i = 4 * (threadIdx.x + u * BS);
+    if (i < K) {
+      float4 v = ld_coherent_f4(x, i);
+      wv[u] = *(const float4 *)(normw + i);
+      *(float4 *)(xs + i) = v;
+      ss += v.x * v.x;
+      ss += v.y * v.y;
+      ss += v.z * v.z;
+      ss += v.w * v.w;
+    }
+  }
+  ss = block_sum<BS>(ss, red);
+  ss /= (float)K;
+  ss += eps;
+  ss = (float)(1.0 / sqrt((double)ss));
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int i = 4 * (threadIdx.x + u * BS);
+    if (i < K) {
+      float4 v = *(float4 *)(xs + i);
+      v.x = wv[u].x * (ss * v.x);
+      v.y = wv[u].y * (ss * v.y);
+      v.z = wv[u].z * (ss * v.z);
+      v.w = wv[u].w * (ss * v.w);
+      *(float4 *)(xs + i) = v;
+    }
   }
   __syncthreads();
 }
 
 __device__ __forceinline__ float silu_ref(float v) { return v / (float)(1.0 + exp((double)(-v))); }
 
-template <int FMT, int KC, int KS, int NR, int MODE>
+// ------------------------------------------------------------------ GEMV
+// Weight tiles stream from HBM straight into LDS (buffer_load_dwordx4 ... lds:
+// no registers are held while a load is in flight) through a ring of DEPTH
+// slots per wave.  A slot holds SC 16-byte chunks per lane plus, for Q8_0, the
+// fp16 block scales of those chunks packed per (row, gate/up) pair.
+//
+// The wait before a slot is read is explicit: s_waitcnt vmcnt(N) with N the
+// number of loads issued after the slot's own (loads complete in issue order).
+// Inside the slot loop a wave issues no other vector-memory operation (the
+// results go to LDS and are written out after the loop), so N is exact.
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+template <int S, int N>
+__device__ __forceinline__ u32x4 *ring_w() {
+  __shared__ __attribute__((aligned(16))) u32x4 a[N];
+  return a;
+}
+template <int S, int N>
+__device__ __forceinline__ unsigned *ring_s() {
+  __shared__ __attribute__((aligned(16))) unsigned a[N];
+  return a;
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N < 63 ? N : 63) : "memory");
+}
+__device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// 16 (4) bytes per lane from rsrc + voff + soff into LDS at lds + 16 (4) * lane.
+#define GL3_DMA_NT 2  // cache policy: nontemporal (weights are read once per token)
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void *lds, unsigned voff, unsigned soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)lds, 16, voff, soff, 0, GL3_DMA_NT);
+}
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, void *lds, unsigned voff, unsigned soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)lds, 4, voff, soff, 0, GL3_DMA_NT);
+}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *p) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, 0x7fffffff, 0x00020000);
+}
+
+template <int FMT, int KC, int KS, int NR, int MODE, int BS, int SC_ = 0, int DEPTH = 2>
 struct GemvPhase {
   typedef ChunkTraits<FMT> T;
   static constexpr int EPC = T::EPC;
-  static constexpr int XPL = KC * EPC;                   // x floats per lane
-  static constexpr int RG = GL3_WAVES_PER_BLOCK / KS;    // row groups per workgroup
+  static constexpr int WPB = BS / GL3_WAVE;
+  static constexpr int RG = WPB / KS;                    // row groups per workgroup
   static constexpr int NP = (MODE == MODE_SWIGLU) ? 2 : 1;
   static constexpr int ROWS_PER_ITEM = RG * NR;          // output rows per work item
+  static constexpr int CHUNKS = NR * NP * KC;            // 16-byte chunks per lane per item
+  // ring slot size (chunks per lane), a multiple of 4
+  static constexpr int SC = SC_ > 0 ? SC_ : ((CHUNKS < 8 ? CHUNKS : 8) + 3) / 4 * 4;
+  static constexpr int JP = (KC < SC / (NR * NP)) ? KC : SC / (NR * NP);  // K-chunks per pass
+  static constexpr int PASSES = (KC + JP - 1) / JP;      // slot loads per item
+  static constexpr int WCH = WPB * SC * GL3_WAVE;        // u32x4 per slot
+  static constexpr int SDW = WPB * SC * 16;              // scale dwords per slot
+  static constexpr int SEG = JP * 64;                    // scale bytes per (row, pair) and pass
+  static constexpr int NSI = FMT == FMT_Q8 ? (NR * NP * SEG + 255) / 256 : 0;  // scale loads per slot
+  static constexpr int JMIN = KC - (PASSES - 1) * JP;    // K-chunks of the last pass
+  static constexpr int NI_MIN = NR * NP * JMIN + NSI;    // fewest loads a slot takes
+  static_assert(WPB % KS == 0, "K-split must divide the waves of a workgroup");
+  static_assert(SC % 4 == 0 && NR * NP <= SC && JP >= 1, "ring slot too small for the rows of a wave");
+  static_assert(DEPTH == 2 || DEPTH == 3, "ring depth");
+  // x of the lane lives in registers when an item is one slot load and the
+  // slice is at most 128 floats; when no norm applies and no two waves share a
+  // slice, each wave loads its slice itself (no LDS staging).
+  static constexpr bool XREG = PASSES == 1 && KC * EPC <= 128;
+  static constexpr bool XDIRECT_OK = XREG && RG == 1;
 
-  struct Tile {
-    u32x4 w[NR][NP][KC];
-    float s[NR][NP][KC];
-  };
-
-  // K-slice of this wave and the element offset of lane chunk j.
   static __device__ __forceinline__ int elem(int K, int ks, int lane, int j) {
     return ks * (K / KS) + EPC * (lane + GL3_WAVE * j);
   }
+  static __host__ __device__ __forceinline__ int items(int out_rows) {
+    return (out_rows + ROWS_PER_ITEM - 1) / ROWS_PER_ITEM;
+  }
+  // items of workgroup blk
+  static __host__ __device__ __forceinline__ int local_items(int out_rows, int blk, int nblk) {
+    const int n = items(out_rows);
+    return blk < n ? (n - 1 - blk) / nblk + 1 : 0;
+  }
+  static __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x / GL3_WAVE); }
 
-  static __device__ __forceinline__ void load_tile(const Mat &W, int out_rows, int item, int rg, int ks, int lane,
-                                                   Tile &t) {
+  // Issues the loads of slot-load u (the workgroup's item u / PASSES, pass u % PASSES) into ring slot S.
+  template <int S>
+  static __device__ __forceinline__ void issue(const Mat &W, int out_rows, int u, int blk, int nblk) {
+    const int wave = wave_id(), lane = threadIdx.x % GL3_WAVE;
+    const int ks = wave % KS, rg = wave / KS;
     const int K = W.cols;
+    const int item = blk + (u / PASSES) * nblk, pass = PASSES > 1 ? u % PASSES : 0;
+    const int j0 = pass * JP;
+    u32x4 *rw = ring_w<S, WCH>() + wave * SC * GL3_WAVE;
+    const __amdgpu_buffer_rsrc_t rq = rsrc(W.q);
+    wait_lds();  // reads of the slot's previous contents have completed
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
       int row = item * ROWS_PER_ITEM + rg * NR + r;
       row = row < out_rows ? row : out_rows - 1;
 #pragma unroll
       for (int p = 0; p < NP; ++p) {
-        const size_t wrow = (size_t)(row + p * out_rows);
+        const unsigned rowoff = (unsigned)((row + p * out_rows) * K + ks * (K / KS) + j0 * GL3_WAVE * EPC) * T::ESZ;
 #pragma unroll
-        for (int j = 0; j < KC; ++j) {
-          const int e = elem(K, ks, lane, j);
-          t.w[r][p][j] = ld_stream(W.q + (wrow * K + e) * T::ESZ);
-          if (FMT == FMT_Q8) t.s[r][p][j] = h2f(W.s[wrow * (K / 32) + e / 32]);
+        for (int jj = 0; jj < JP; ++jj) {
+          if (PASSES > 1 && j0 + jj >= KC) break;
+          dma16(rq, rw + ((r * NP + p) * JP + jj) * GL3_WAVE, 16u * lane, rowoff + jj * GL3_WAVE * 16);
         }
+      }
+    }
+    if (FMT == FMT_Q8) {
+      // scales: NR*NP segments of SEG bytes (the pass's chunks), 4 bytes per lane per load
+      constexpr int TOTAL = NR * NP * SEG;
+      const int valid = (PASSES > 1 && KC - j0 < JP) ? (KC - j0) * 64 : SEG;
+      unsigned *rs = ring_s<S, SDW>() + wave * SC * 16;
+      const __amdgpu_buffer_rsrc_t rsc = rsrc(W.s);
+#pragma unroll
+      for (int i = 0; i < NSI; ++i) {
+        int b = 256 * i + 4 * lane;
+        b = b < TOTAL ? b : TOTAL - 4;
+        const int rp = b / SEG;
+        int off = b % SEG;
+        off = off < valid ? off : valid - 4;
+        int row = item * ROWS_PER_ITEM + rg * NR + rp / NP;
+        row = row < out_rows ? row : out_rows - 1;
+        const unsigned voff = (unsigned)(row + (rp % NP) * out_rows) * (unsigned)(K / 16) + (unsigned)off;
+        dma4(rsc, rs + i * GL3_WAVE, voff, (unsigned)(ks * (K / KS) / 16 + j0 * 64));
       }
     }
   }
 
-  // Partial dot products of the lane for every (row, pair).
-  static __device__ __forceinline__ void dot_tile(const Tile &t, const float (&xr)[KC][EPC], float (&acc)[NR][NP]) {
+  // Loads of the workgroup's first DEPTH slot-loads, issued ahead (e.g. while
+  // the grid barrier before the phase is still open).
+  static __device__ __forceinline__ void prefetch(const Mat &W, int out_rows, int blk, int nblk) {
+    const int nu = local_items(out_rows, blk, nblk) * PASSES;
+    if (nu > 0) issue<0>(W, out_rows, 0, blk, nblk);
+    if (nu > 1) issue<1>(W, out_rows, 1, blk, nblk);
+    if (DEPTH == 3 && nu > 2) issue<(DEPTH == 3 ? 2 : 1)>(W, out_rows, 2, blk, nblk);
+  }
+
+  struct XSlice {
+    float r[XREG ? KC : 1][XREG ? EPC : 1];
+    const float *lds;
+    int e0;
+    __device__ __forceinline__ float get(int j, int i) const {
+      return XREG ? r[XREG ? j : 0][XREG ? i : 0] : lds[e0 + GL3_WAVE * EPC * j + i];
+    }
+  };
+
+  // acc[r][p] += the lane's part of the dot products held in slot S (pass `pass` of the item)
+  template <int S>
+  static __device__ __forceinline__ void dot_slot(const XSlice &xr, int pass, float (&acc)[NR][NP]) {
+    const int wave = wave_id(), lane = threadIdx.x % GL3_WAVE;
+    const u32x4 *rw = ring_w<S, WCH>() + wave * SC * GL3_WAVE + lane;
+    const uint8_t *rs = (const uint8_t *)(ring_s<S, SDW>() + wave * SC * 16);
+    const int j0 = pass * JP;
 #pragma unroll
     for (int r = 0; r < NR; ++r)
 #pragma unroll
       for (int p = 0; p < NP; ++p) {
-        float a = 0.0f;
+        float a = acc[r][p];
 #pragma unroll
-        for (int j = 0; j < KC; ++j) {
-          const u32x4 w = t.w[r][p][j];
+        for (int jj = 0; jj < JP; ++jj) {
+          if (PASSES > 1 && j0 + jj >= KC) break;
+          const int c = (r * NP + p) * JP + jj;
+          const int j = PASSES > 1 ? j0 + jj : jj;
+          const u32x4 w = rw[c * GL3_WAVE];
+          const unsigned ww[4] = {w.x, w.y, w.z, w.w};
           if (FMT == FMT_Q8) {
-            float c = 0.0f;
-            const unsigned ww[4] = {w.x, w.y, w.z, w.w};
+            const float sc = h2f(*(const uint16_t *)(rs + (r * NP + p) * SEG + ((lane + GL3_WAVE * jj) & ~1)));
+            float cacc = 0.0f;
 #pragma unroll
             for (int d = 0; d < 4; ++d) {
-              c = fmaf(sbyte<0>(ww[d]), xr[j][4 * d + 0], c);
-              c = fmaf(sbyte<1>(ww[d]), xr[j][4 * d + 1], c);
-              c = fmaf(sbyte<2>(ww[d]), xr[j][4 * d + 2], c);
-              c = fmaf(sbyte<3>(ww[d]), xr[j][4 * d + 3], c);
+              cacc = fmaf(sbyte<0>(ww[d]), xr.get(j, 4 * d + 0), cacc);
+              cacc = fmaf(sbyte<1>(ww[d]), xr.get(j, 4 * d + 1), cacc);
+              cacc = fmaf(sbyte<2>(ww[d]), xr.get(j, 4 * d + 2), cacc);
+              cacc = fmaf(sbyte<3>(ww[d]), xr.get(j, 4 * d + 3), cacc);
             }
-            a = fmaf(t.s[r][p][j], c, a);
+            a = fmaf(sc, cacc, a);
           } else {
-            const unsigned ww[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
             for (int d = 0; d < 4; ++d) {
-              a = fmaf(h2f_lo(ww[d]), xr[j][2 * d + 0], a);
-              a = fmaf(h2f_hi(ww[d]), xr[j][2 * d + 1], a);
+              a = fmaf(h2f_lo(ww[d]), xr.get(j, 2 * d + 0), a);
+              a = fmaf(h2f_hi(ww[d]), xr.get(j, 2 * d + 1), a);
             }
           }
         }
@@ -269,112 +440,199 @@ struct GemvPhase {
       }
   }
 
-  // Runs the phase.  x: input vector (K floats, coherent); normw: RMSNorm
-  // weights or nullptr; y: output (MODE_RESIDUAL: y += W n(x)); for
-  // MODE_LOGITS, y gets the rows and best_out[blk] the argmax key of the rows
-  // this workgroup produced.
-  static __device__ void run(const Mat &W, int out_rows, const float *x, const float *normw, float eps, float *y,
-                             unsigned long long *best_out, int blk, int nblk, float *lds) {
-    const int K = W.cols;
-    float *xs = lds;                 // K floats
-    float *red = lds + K;            // reduction scratch
-    float *kpart = red + 16;         // [RG][NR][NP][KS] cross-wave partials
-    load_x_lds(x, normw, eps, K, xs, red);
-
-    const int wave = threadIdx.x / GL3_WAVE, lane = threadIdx.x % GL3_WAVE;
+  // Reduces and combines the K-split partials of the workgroup's i-th item;
+  // the row values go to obuf[i * ROWS_PER_ITEM + row in item].
+  static __device__ __forceinline__ void finish_item(int i, float (&acc)[NR][NP], float *kpart, float *obuf) {
+    const int wave = wave_id(), lane = threadIdx.x % GL3_WAVE;
     const int ks = wave % KS, rg = wave / KS;
-    float xr[KC][EPC];
 #pragma unroll
-    for (int j = 0; j < KC; ++j) {
-      const int e = elem(K, ks, lane, j);
+    for (int r = 0; r < NR; ++r)
 #pragma unroll
-      for (int i = 0; i < EPC; ++i) xr[j][i] = xs[e + i];
-    }
-
-    const int n_items = (out_rows + ROWS_PER_ITEM - 1) / ROWS_PER_ITEM;
-    unsigned long long best = 0;
-    int item = blk;
-    Tile cur;
-    if (item < n_items) load_tile(W, out_rows, item, rg, ks, lane, cur);
-    for (; item < n_items; item += nblk) {
-      Tile nxt;
-      const int next = item + nblk;
-      if (next < n_items) load_tile(W, out_rows, next, rg, ks, lane, nxt);
-      float acc[NR][NP];
-      dot_tile(cur, xr, acc);
-#pragma unroll
-      for (int r = 0; r < NR; ++r)
-#pragma unroll
-        for (int p = 0; p < NP; ++p) acc[r][p] = wave_sum(acc[r][p]);
-      if (KS > 1) {
-        if (lane == 0) {
-#pragma unroll
-          for (int r = 0; r < NR; ++r)
-#pragma unroll
-            for (int p = 0; p < NP; ++p) kpart[((rg * NR + r) * NP + p) * KS + ks] = acc[r][p];
-        }
-        __syncthreads();
+      for (int p = 0; p < NP; ++p) acc[r][p] = wave_sum(acc[r][p]);
+    if (KS > 1) {
+      if (lane == 0) {
 #pragma unroll
         for (int r = 0; r < NR; ++r)
 #pragma unroll
-          for (int p = 0; p < NP; ++p) {
-            float s = 0.0f;
-#pragma unroll
-            for (int q = 0; q < KS; ++q) s += kpart[((rg * NR + r) * NP + p) * KS + q];
-            acc[r][p] = s;
-          }
-        __syncthreads();
+          for (int p = 0; p < NP; ++p) kpart[((rg * NR + r) * NP + p) * KS + ks] = acc[r][p];
       }
-      if (lane == 0 && ks == 0) {
+      __syncthreads();
 #pragma unroll
-        for (int r = 0; r < NR; ++r) {
-          const int row = item * ROWS_PER_ITEM + rg * NR + r;
-          if (row < out_rows) {
-            if (MODE == MODE_STORE) {
-              st_coherent(y + row, acc[r][0]);
-            } else if (MODE == MODE_RESIDUAL) {
-              st_coherent(y + row, ld_coherent(y + row) + acc[r][0]);
-            } else if (MODE == MODE_SWIGLU) {
-              st_coherent(y + row, silu_ref(acc[r][0]) * acc[r][NP - 1]);
-            } else {
-              y[row] = acc[r][0];
-              unsigned long long k = argmax_key(acc[r][0], row);
-              best = k > best ? k : best;
-            }
+      for (int r = 0; r < NR; ++r)
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          float s = 0.0f;
+#pragma unroll
+          for (int q = 0; q < KS; ++q) s += kpart[((rg * NR + r) * NP + p) * KS + q];
+          acc[r][p] = s;
+        }
+      __syncthreads();
+    }
+    if (ks == 0 && lane < NR) {
+      float a0 = acc[0][0], a1 = acc[0][NP - 1];
+#pragma unroll
+      for (int r = 1; r < NR; ++r)
+        if (lane == r) {
+          a0 = acc[r][0];
+          a1 = acc[r][NP - 1];
+        }
+      obuf[i * ROWS_PER_ITEM + rg * NR + lane] = (MODE == MODE_SWIGLU) ? silu_ref(a0) * a1 : a0;
+    }
+  }
+
+  template <int S>
+  static __device__ __forceinline__ void step(const Mat &W, int out_rows, int u, int nu, int blk, int nblk,
+                                              const XSlice &xr, float (&acc)[NR][NP], float *kpart, float *obuf) {
+    if (u < nu) {
+      // slot S is complete once at most the loads of the (up to DEPTH-1) later slot-loads are outstanding
+      const int later = nu - 1 - u;
+      if (DEPTH == 3 && later >= 2)
+        wait_vmem<2 * NI_MIN>();
+      else if (later >= 1)
+        wait_vmem<NI_MIN>();
+      else
+        wait_vmem<0>();
+      const int pass = PASSES > 1 ? u % PASSES : 0;
+      dot_slot<S>(xr, pass, acc);
+      if (u + DEPTH < nu) issue<S>(W, out_rows, u + DEPTH, blk, nblk);
+      if (PASSES == 1 || pass == PASSES - 1) {
+        finish_item(u / PASSES, acc, kpart, obuf);
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+#pragma unroll
+          for (int p = 0; p < NP; ++p) acc[r][p] = 0.0f;
+      }
+    }
+  }
+
+  // LDS layout of a phase: [x (K floats, when staged)] [red 32] [kpart] [obuf] [best keys]
+  static __host__ __device__ constexpr int kpart_floats() { return RG * NR * NP * KS; }
+  static __host__ __device__ __forceinline__ bool staged(bool has_norm) { return !(XDIRECT_OK && !has_norm); }
+  static __host__ __device__ __forceinline__ size_t lds_bytes(int K, int out_rows, int nblk, bool has_norm) {
+    const int lr = local_items(out_rows, 0, nblk) * ROWS_PER_ITEM;
+    return (size_t)((staged(has_norm) ? K : 0) + 32 + kpart_floats() + lr + 2 * WPB + 4) * sizeof(float);
+  }
+
+  // Runs the phase.  x: input vector (K floats, coherent); normw: RMSNorm
+  // weights or nullptr; y: output (MODE_RESIDUAL: y += W n(x)); for
+  // MODE_LOGITS, y gets the rows and best_out[blk] the argmax key of the rows
+  // this workgroup produced.  prefetched: prefetch() was already called with
+  // the same W, out_rows, blk and nblk.
+  static __device__ void run(const Mat &W, int out_rows, const float *x, const float *normw, float eps, float *y,
+                             unsigned long long *best_out, int blk, int nblk, float *lds, bool prefetched = false) {
+    const int K = W.cols;
+    const bool stg = staged(normw != nullptr);
+    float *xs = lds;                          // K floats when staged
+    float *red = lds + (stg ? K : 0);         // reduction scratch (32 floats)
+    float *kpart = red + 32;                  // cross-wave partials
+    float *obuf = kpart + kpart_floats();     // row values of the workgroup's items
+    const int nli = local_items(out_rows, blk, nblk);
+    const int nu = nli * PASSES;
+    if (!prefetched) prefetch(W, out_rows, blk, nblk);
+
+    const int wave = wave_id(), lane = threadIdx.x % GL3_WAVE;
+    const int ks = wave % KS;
+    XSlice xr;
+    xr.lds = xs;
+    xr.e0 = elem(K, ks, lane, 0);
+    if (!stg) {
+      if (XDIRECT_OK) {
+#pragma unroll
+        for (int j = 0; j < KC; ++j)
+#pragma unroll
+          for (int i = 0; i < EPC; i += 4) {
+            const float4 v = ld_coherent_f4(x, (unsigned)(elem(K, ks, lane, j) + i));
+            xr.r[j][i] = v.x;
+            xr.r[j][i + 1] = v.y;
+            xr.r[j][i + 2] = v.z;
+            xr.r[j][i + 3] = v.w;
+          }
+      }
+    } else {
+      load_x_lds<BS>(x, normw, eps, K, xs, red);
+      if (XREG) {
+#pragma unroll
+        for (int j = 0; j < KC; ++j) {
+          const int e = elem(K, ks, lane, j);
+#pragma unroll
+          for (int i = 0; i < EPC; i += 4) {
+            float4 v = *(const float4 *)(xs + e + i);
+            xr.r[j][i] = v.x;
+            xr.r[j][i + 1] = v.y;
+            xr.r[j][i + 2] = v.z;
+            xr.r[j][i + 3] = v.w;
           }
         }
       }
-      if (next < n_items) cur = nxt;
+    }
+
+    float acc[NR][NP];
+#pragma unroll
+    for (int r = 0; r < NR; ++r)
+#pragma unroll
+      for (int p = 0; p < NP; ++p) acc[r][p] = 0.0f;
+    for (int u = 0; u < nu; u += DEPTH) {
+      step<0>(W, out_rows, u, nu, blk, nblk, xr, acc, kpart, obuf);
+      step<1>(W, out_rows, u + 1, nu, blk, nblk, xr, acc, kpart, obuf);
+      if (DEPTH == 3) step<(DEPTH == 3 ? 2 : 1)>(W, out_rows, u + 2, nu, blk, nblk, xr, acc, kpart, obuf);
+    }
+    __syncthreads();
+
+    // write the rows out (coalesced over the workgroup's items)
+    unsigned long long best = 0;
+    for (int lr = threadIdx.x; lr < nli * ROWS_PER_ITEM; lr += BS) {
+      const int row = (blk + (lr / ROWS_PER_ITEM) * nblk) * ROWS_PER_ITEM + lr % ROWS_PER_ITEM;
+      if (row < out_rows) {
+        const float v = obuf[lr];
+        if (MODE == MODE_RESIDUAL) {
+          st_coherent(y + row, ld_coherent(y + row) + v);
+        } else if (MODE == MODE_LOGITS) {
+          y[row] = v;
+          const unsigned long long k = argmax_key(v, row);
+          best = k > best ? k : best;
+        } else {
+          st_coherent(y + row, v);
+        }
+      }
     }
     if (MODE == MODE_LOGITS) {
-      __shared__ unsigned long long bred[GL3_WAVES_PER_BLOCK];
+      unsigned long long *bred = (unsigned long long *)(obuf + nli * ROWS_PER_ITEM + 1);
+      bred = (unsigned long long *)(((uintptr_t)bred + 7) & ~(uintptr_t)7);
+      for (int o = 32; o >= 1; o >>= 1) {
+        unsigned long long other = __shfl_xor(best, o);
+        best = other > best ? other : best;
+      }
       if (lane == 0) bred[wave] = best;
       __syncthreads();
       if (threadIdx.x == 0) {
         unsigned long long b = 0;
-        for (int w = 0; w < GL3_WAVES_PER_BLOCK; ++w) b = bred[w] > b ? bred[w] : b;
+        for (int w = 0; w < WPB; ++w) b = bred[w] > b ? bred[w] : b;
         __hip_atomic_store(best_out + blk, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
     __syncthreads();  // LDS is reused by the next phase
   }
-
-  static constexpr size_t lds_bytes(int K) { return (size_t)(K + 16 + RG * NR * NP * KS + 16) * sizeof(float); }
 };
 
 // -------------------------------------------------------------- attention
-// Flash-decode over the fp16 KV cache [L][n_kv][ctx][hd].  Work item = (kv head,
-// split of positions); the workgroup serves every query head of the kv head's
-// GQA group, so each K/V row is read from HBM once per group.  K and V tiles of
-// ATT_TILE positions are staged in LDS (converted to fp32 once); scores use the
-// reference's order of operations (sequential dot, then / sqrt(hd), InferenceCore.java:114-121),
-// softmax is online within the split and splits merge by log-sum-exp in the
-// workgroup that finishes last.  The same workgroup applies the Qwen3 per-head
-// RMSNorm and RoPE to q and, for the split holding `pos`, to k, and appends k,v
-// to the cache (InferenceCore.java:82-100, :341-372, :472-491).
+// Flash-decode over the fp16 KV cache [L][n_kv][ctx][hd].  Work item = (kv
+// head, split of positions); the workgroup serves the GQ query heads of the kv
+// head's GQA group, so each K/V row is read from HBM once per group.
+//
+// Inside a work item every wavefront owns positions in steps of PPW = 64/LP:
+// LP lanes read one position's K and V row with 16-byte loads (8 fp16 each),
+// hold q in registers, reduce the GQ scores over the LP lanes with DPP and keep
+// an online softmax state (max, sum, o) per lane group in registers.  The lane
+// groups of a wave are merged with shuffles, the waves through LDS, and the
+// splits of a kv head by log-sum-exp in the workgroup that finishes last.
+//
+// Scores are (q . k) / sqrt(hd) (InferenceCore.java:114-121).  The same
+// workgroup applies the Qwen3 per-head RMSNorm and RoPE to q and, for the split
+// holding `pos`, to k, and appends k,v to the cache (InferenceCore.java:82-100,
+// :341-372, :472-491).
 
-#define ATT_TILE 64
 #define ATT_MAX_G 8
+#define ATT_UNROLL 2
 
 __device__ __forceinline__ void rope_pair(float &v0, float &v1, float c, float s) {
   float a = v0 * c - v1 * s;
@@ -384,16 +642,17 @@ __device__ __forceinline__ void rope_pair(float &v0, float &v1, float c, float s
 }
 
 // Prepare `nvec` head vectors of length hd from src (coherent) into dst (LDS):
-// optional per-head RMSNorm, then RoPE at pos.  Caller must __syncthreads() after.
+// optional per-head RMSNorm, then RoPE at pos.  Ends with __syncthreads().
+template <int BS>
 __device__ inline void prep_heads(const ModelDev &m, const float *src, int nvec, const float *normw, int pos,
-                                  float *dst, float *red) {
+                                  float *dst) {
   const int hd = m.hd, half = hd / 2;
-  for (int i = threadIdx.x; i < nvec * hd; i += GL3_BLOCK) dst[i] = ld_coherent(src + i);
+  for (int i = 4 * threadIdx.x; i < nvec * hd; i += 4 * BS) *(float4 *)(dst + i) = ld_coherent_f4(src, i);
   __syncthreads();
   if (normw) {
-    // one wave per head vector: ss = sum x^2; x = w * (ss * x)   (Qwen3Kernels / InferenceCore.java:341-347)
+    // one wave per head vector: ss = sum x^2; x = w * (ss * x)   (InferenceCore.java:341-347)
     const int wave = threadIdx.x / GL3_WAVE, lane = threadIdx.x % GL3_WAVE;
-    for (int g = wave; g < nvec; g += GL3_WAVES_PER_BLOCK) {
+    for (int g = wave; g < nvec; g += BS / GL3_WAVE) {
       float ss = 0.0f;
       for (int d = lane; d < hd; d += GL3_WAVE) ss += dst[g * hd + d] * dst[g * hd + d];
       ss = wave_sum(ss);
@@ -405,7 +664,7 @@ __device__ inline void prep_heads(const ModelDev &m, const float *src, int nvec,
     __syncthreads();
   }
   const float *cr = m.rope_cos + (size_t)pos * half, *ci = m.rope_sin + (size_t)pos * half;
-  for (int t = threadIdx.x; t < nvec * half; t += GL3_BLOCK) {
+  for (int t = threadIdx.x; t < nvec * half; t += BS) {
     const int g = t / half, i = t % half;
     int i0, i1;
     if (m.family == FAM_LLAMA) { i0 = 2 * i; i1 = 2 * i + 1; }
@@ -415,177 +674,231 @@ __device__ inline void prep_heads(const ModelDev &m, const float *src, int nvec,
     dst[g * hd + i0] = v0;
     dst[g * hd + i1] = v1;
   }
+  __syncthreads();
 }
 
-__device__ inline int att_split_len(const ModelDev &m, int pos) {
-  const int n = pos + 1;
-  int s = (n + m.max_split - 1) / m.max_split;
-  s = (s + ATT_TILE - 1) / ATT_TILE * ATT_TILE;
-  return s < ATT_TILE ? ATT_TILE : s;
+// Positions per split: a multiple of the workgroup's positions per step.
+__host__ __device__ __forceinline__ int att_split_len(int n, int max_split, int step) {
+  int s = (n + max_split - 1) / max_split;
+  s = (s + step - 1) / step * step;
+  return s < step ? step : s;
 }
 
-__device__ inline size_t att_lds_floats(int hd, int G) {
-  return (size_t)G * hd            // q
-         + 2 * hd                  // new k, v
-         + ATT_TILE * (hd + 1)     // K tile (padded rows)
-         + ATT_TILE * hd           // V tile
-         + G * ATT_TILE            // p
-         + 3 * ATT_MAX_G + 16;     // m, l, scale, flags
+// LDS floats of the attention phase: q, new k/v, per-wave partials or merge weights, flag.
+__host__ __device__ __forceinline__ int att_region_floats(int hd, int G, int wpb, int max_split) {
+  const int wparts = wpb * G * (hd + 4);
+  const int merge = 2 * G * max_split + G + 8;
+  return wparts > merge ? wparts : merge;
+}
+__host__ __device__ __forceinline__ int att_lds_floats(int hd, int G, int wpb, int max_split) {
+  return G * hd + 2 * hd + att_region_floats(hd, G, wpb, max_split) + 16;
 }
 
+template <int GQ>
+__device__ __forceinline__ void online_update(float (&mr)[GQ], float (&lr)[GQ], float (&o)[GQ][8], const float (&s)[GQ],
+                                              const float (&vf)[8]) {
+#pragma unroll
+  for (int g = 0; g < GQ; ++g) {
+    const float mn = fmaxf(mr[g], s[g]);
+    const float c = __expf(mr[g] - mn);
+    const float p = __expf(s[g] - mn);
+    lr[g] = lr[g] * c + p;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[g][i] = fmaf(p, vf[i], o[g][i] * c);
+    mr[g] = mn;
+  }
+}
+
+// Merge (m, l, o) of lane groups `mask` apart within the wave.
+template <int GQ>
+__device__ __forceinline__ void merge_lanes(float (&mr)[GQ], float (&lr)[GQ], float (&o)[GQ][8], int mask) {
+#pragma unroll
+  for (int g = 0; g < GQ; ++g) {
+    const float m2 = __shfl_xor(mr[g], mask), l2 = __shfl_xor(lr[g], mask);
+    const float mn = fmaxf(mr[g], m2);
+    const float c1 = (mn == -INFINITY) ? 0.0f : __expf(mr[g] - mn);
+    const float c2 = (mn == -INFINITY) ? 0.0f : __expf(m2 - mn);
+    lr[g] = lr[g] * c1 + l2 * c2;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float o2 = __shfl_xor(o[g][i], mask);
+      o[g][i] = o[g][i] * c1 + o2 * c2;
+    }
+    mr[g] = mn;
+  }
+}
+
+template <int LP, int GQ, int BS>
 __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, int nblk, float *lds) {
-  const int hd = m.hd, G = m.n_heads / m.n_kv, kv_dim = m.kv_dim;
-  const int S = att_split_len(m, pos);
+  constexpr int WPB = BS / GL3_WAVE, PPW = GL3_WAVE / LP, PPB = PPW * WPB;
+  const int hd = m.hd, kv_dim = m.kv_dim;
   const int n = pos + 1;
+  const int S = att_split_len(n, m.max_split, PPB * ATT_UNROLL);
   const int nsplit = (n + S - 1) / S;
   const int items = m.n_kv * nsplit;
-  const int hdp = hd + 1;
-  float *qs = lds;
-  float *knew = qs + G * hd;
-  float *vnew = knew + hd;
-  float *kt = vnew + hd;
-  float *vt = kt + ATT_TILE * hdp;
-  float *ps = vt + ATT_TILE * hd;
-  float *ml = ps + G * ATT_TILE;   // m[G], l[G], scale[G]
-  int *flag = (int *)(ml + 3 * ATT_MAX_G);
-  float *red = (float *)(flag + 8);
+  const int hpart = hd + 4;
+  float *qs = lds;                 // [GQ][hd]
+  float *knew = qs + GQ * hd;      // [hd]
+  float *vnew = knew + hd;         // [hd]
+  float *wp = vnew + hd;           // per-wave partials [WPB][GQ][hd + 4], then merge weights
+  int *flag = (int *)(wp + att_region_floats(hd, GQ, WPB, m.max_split));
   const LayerDev &L = m.layers[layer];
   const size_t head_stride = (size_t)m.ctx * hd;
   uint16_t *kc_l = m.kc + (size_t)layer * m.n_kv * head_stride;
   uint16_t *vc_l = m.vc + (size_t)layer * m.n_kv * head_stride;
+  const int wave = threadIdx.x / GL3_WAVE, lane = threadIdx.x % GL3_WAVE;
+  const int grp = lane / LP, sub = lane % LP, d0 = 8 * sub;
+  const bool act = d0 < hd;
 
   for (int item = blk; item < items; item += nblk) {
     const int kvh = item / nsplit, sp = item % nsplit;
     const int t0 = sp * S, t1 = min(n, t0 + S);
     uint16_t *kh = kc_l + kvh * head_stride;
     uint16_t *vh = vc_l + kvh * head_stride;
-    // q of the group's heads (contiguous in qkv), normalised and rotated
-    prep_heads(m, m.qkv + (size_t)kvh * G * hd, G, m.family == FAM_QWEN3 ? L.q_norm : nullptr, pos, qs, red);
+    // K/V rows of the first step do not depend on q: load them before preparing q
+    u32x4 kw[ATT_UNROLL], vw[ATT_UNROLL];
+    const int tb0 = t0 + wave * PPW;
+#pragma unroll
+    for (int u = 0; u < ATT_UNROLL; ++u) {
+      const int t = tb0 + u * PPB + grp;
+      if (act && t < t1 && t != pos) {
+        kw[u] = ld_stream(kh + (size_t)t * hd + d0);
+        vw[u] = ld_stream(vh + (size_t)t * hd + d0);
+      } else {
+        kw[u] = u32x4{0u, 0u, 0u, 0u};
+        vw[u] = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+    prep_heads<BS>(m, m.qkv + (size_t)kvh * GQ * hd, GQ, m.family == FAM_QWEN3 ? L.q_norm : nullptr, pos, qs);
     const bool owns_pos = (pos >= t0 && pos < t1);
     if (owns_pos) {
+      prep_heads<BS>(m, m.qkv + m.q_dim + (size_t)kvh * hd, 1, m.family == FAM_QWEN3 ? L.k_norm : nullptr, pos,
+                     knew);
+      for (int d = 4 * threadIdx.x; d < hd; d += 4 * BS)
+        *(float4 *)(vnew + d) = ld_coherent_f4(m.qkv, m.q_dim + kv_dim + kvh * hd + d);
       __syncthreads();
-      prep_heads(m, m.qkv + m.q_dim + (size_t)kvh * hd, 1, m.family == FAM_QWEN3 ? L.k_norm : nullptr, pos, knew, red);
-      for (int d = threadIdx.x; d < hd; d += GL3_BLOCK) vnew[d] = ld_coherent(m.qkv + m.q_dim + kv_dim + (size_t)kvh * hd + d);
-      __syncthreads();
-      for (int d = threadIdx.x; d < hd; d += GL3_BLOCK) {
+      for (int d = threadIdx.x; d < hd; d += BS) {
         uint16_t kh16 = f2h(knew[d]), vh16 = f2h(vnew[d]);
         kh[(size_t)pos * hd + d] = kh16;
         vh[(size_t)pos * hd + d] = vh16;
         knew[d] = h2f(kh16);
         vnew[d] = h2f(vh16);
       }
+      __syncthreads();
     }
-    if (threadIdx.x < G) {
-      ml[threadIdx.x] = -INFINITY;
-      ml[ATT_MAX_G + threadIdx.x] = 0.0f;
+    // q slice of this lane, all heads of the group
+    float qr[GQ][8];
+#pragma unroll
+    for (int g = 0; g < GQ; ++g)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qr[g][i] = act ? qs[g * hd + d0 + i] : 0.0f;
+    float mr[GQ], lr[GQ], o[GQ][8];
+#pragma unroll
+    for (int g = 0; g < GQ; ++g) {
+      mr[g] = -INFINITY;
+      lr[g] = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[g][i] = 0.0f;
     }
-    // output accumulators: thread handles (g, d) pairs idx = threadIdx.x + k*GL3_BLOCK
-    float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    const int npairs = G * hd;
-    __syncthreads();
-
-    for (int tt = t0; tt < t1; tt += ATT_TILE) {
-      const int nt = min(ATT_TILE, t1 - tt);
-      // stage K and V rows [tt, tt+nt) as fp32; 8 halfs (16 bytes) per load
-      const int chunks = ATT_TILE * hd / 8;
-      for (int c = threadIdx.x; c < chunks; c += GL3_BLOCK) {
-        const int t = (c * 8) / hd, d0 = (c * 8) % hd;
-        const int tp = tt + t;
+    for (int tb = tb0; tb < t1; tb += ATT_UNROLL * PPB) {
+      if (tb != tb0) {
+#pragma unroll
+        for (int u = 0; u < ATT_UNROLL; ++u) {
+          const int t = tb + u * PPB + grp;
+          if (act && t < t1 && t != pos) {
+            kw[u] = ld_stream(kh + (size_t)t * hd + d0);
+            vw[u] = ld_stream(vh + (size_t)t * hd + d0);
+          } else {
+            kw[u] = u32x4{0u, 0u, 0u, 0u};
+            vw[u] = u32x4{0u, 0u, 0u, 0u};
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < ATT_UNROLL; ++u) {
+        const int t = tb + u * PPB + grp;
         float kf[8], vf[8];
-        if (t < nt && tp != pos) {
-          u32x4 kw = ld_stream(kh + (size_t)tp * hd + d0);
-          u32x4 vw = ld_stream(vh + (size_t)tp * hd + d0);
-          const unsigned ka[4] = {kw.x, kw.y, kw.z, kw.w}, va[4] = {vw.x, vw.y, vw.z, vw.w};
+        if (t == pos && act) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) { kf[i] = knew[d0 + i]; vf[i] = vnew[d0 + i]; }
+        } else {
+          const unsigned ka[4] = {kw[u].x, kw[u].y, kw[u].z, kw[u].w}, va[4] = {vw[u].x, vw[u].y, vw[u].z, vw[u].w};
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             kf[2 * i] = h2f_lo(ka[i]); kf[2 * i + 1] = h2f_hi(ka[i]);
             vf[2 * i] = h2f_lo(va[i]); vf[2 * i + 1] = h2f_hi(va[i]);
           }
-        } else if (t < nt) {
+        }
+        float s[GQ];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) { kf[i] = knew[d0 + i]; vf[i] = vnew[d0 + i]; }
-        } else {
+        for (int g = 0; g < GQ; ++g) {
+          float a = 0.0f;
 #pragma unroll
-          for (int i = 0; i < 8; ++i) { kf[i] = 0.0f; vf[i] = 0.0f; }
+          for (int i = 0; i < 8; ++i) a = fmaf(qr[g][i], kf[i], a);
+          s[g] = group_sum<LP>(a) / m.sqrt_hd;
         }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          kt[t * hdp + d0 + i] = kf[i];
-          vt[t * hd + d0 + i] = vf[i];
-        }
+        if (t < t1) online_update<GQ>(mr, lr, o, s, vf);
       }
-      __syncthreads();
-      // scores: thread (t, g)
-      for (int idx = threadIdx.x; idx < G * ATT_TILE; idx += GL3_BLOCK) {
-        const int t = idx % ATT_TILE, g = idx / ATT_TILE;
-        float s = -INFINITY;
-        if (t < nt) {
-          const float *q = qs + g * hd, *k = kt + t * hdp;
-          float acc = 0.0f;
-          for (int d = 0; d < hd; ++d) acc += q[d] * k[d];
-          s = acc / m.sqrt_hd;
-        }
-        ps[g * ATT_TILE + t] = s;
-      }
-      __syncthreads();
-      // online softmax per head: one wave per head
-      {
-        const int wave = threadIdx.x / GL3_WAVE, lane = threadIdx.x % GL3_WAVE;
-        for (int g = wave; g < G; g += GL3_WAVES_PER_BLOCK) {
-          float s = ps[g * ATT_TILE + lane];  // ATT_TILE == GL3_WAVE
-          float mt = wave_max(s);
-          float mold = ml[g];
-          float mnew = fmaxf(mold, mt);
-          float p = (lane < nt) ? expf(s - mnew) : 0.0f;
-          ps[g * ATT_TILE + lane] = p;
-          float lsum = wave_sum(p);
-          float scale = expf(mold - mnew);  // exp(-inf) = 0 on the first tile
-          if (lane == 0) {
-            ml[g] = mnew;
-            ml[ATT_MAX_G + g] = ml[ATT_MAX_G + g] * scale + lsum;
-            ml[2 * ATT_MAX_G + g] = scale;
-          }
-        }
-      }
-      __syncthreads();
-      // o[g][d] = o * scale + sum_t p[g][t] * V[t][d]
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int idx = threadIdx.x + k * GL3_BLOCK;
-        if (idx < npairs) {
-          const int g = idx / hd, d = idx % hd;
-          float acc = o[k] * ml[2 * ATT_MAX_G + g];
-          for (int t = 0; t < nt; ++t) acc += ps[g * ATT_TILE + t] * vt[t * hd + d];
-          o[k] = acc;
-        }
-      }
-      __syncthreads();
     }
-
-    // write the result of this split
-    const int hpart = hd + 2;
+    // merge the lane groups of the wave, then the waves of the workgroup
+#pragma unroll
+    for (int mask = LP; mask < GL3_WAVE; mask <<= 1) merge_lanes<GQ>(mr, lr, o, mask);
+    if (grp == 0 && act) {
+#pragma unroll
+      for (int g = 0; g < GQ; ++g) {
+        float *dst = wp + (wave * GQ + g) * hpart;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) dst[d0 + i] = o[g][i];
+        if (sub == 0) {
+          dst[hd] = mr[g];
+          dst[hd + 1] = lr[g];
+        }
+      }
+    }
+    __syncthreads();
+    // thread (g, d) pairs: combine the WPB wave partials (GQ * hd <= 4 * BS, checked by the host)
+    constexpr int PAIRS = (GQ * 128 + BS - 1) / BS;  // per-thread slots for hd <= 128
+    float Ofin[PAIRS], Mfin[PAIRS], Lfin[PAIRS];
+#pragma unroll
+    for (int k = 0; k < PAIRS; ++k) {
+      Ofin[k] = 0.0f;
+      Mfin[k] = -INFINITY;
+      Lfin[k] = 0.0f;
+      const int idx = threadIdx.x + k * BS;
+      if (idx < GQ * hd) {
+        const int g = idx / hd, d = idx % hd;
+        for (int w = 0; w < WPB; ++w) Mfin[k] = fmaxf(Mfin[k], wp[(w * GQ + g) * hpart + hd]);
+        for (int w = 0; w < WPB; ++w) {
+          const float *src = wp + (w * GQ + g) * hpart;
+          const float c = (src[hd] == -INFINITY) ? 0.0f : __expf(src[hd] - Mfin[k]);
+          Lfin[k] += src[hd + 1] * c;
+          Ofin[k] += src[d] * c;
+        }
+      }
+    }
+    __syncthreads();
     if (nsplit == 1) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int idx = threadIdx.x + k * GL3_BLOCK;
-        if (idx < npairs) {
+      for (int k = 0; k < PAIRS; ++k) {
+        const int idx = threadIdx.x + k * BS;
+        if (idx < GQ * hd) {
           const int g = idx / hd, d = idx % hd;
-          st_coherent(m.att + (size_t)(kvh * G + g) * hd + d, o[k] / ml[ATT_MAX_G + g]);
+          st_coherent(m.att + (size_t)(kvh * GQ + g) * hd + d, Ofin[k] / Lfin[k]);
         }
       }
     } else {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int idx = threadIdx.x + k * GL3_BLOCK;
-        if (idx < npairs) {
+      for (int k = 0; k < PAIRS; ++k) {
+        const int idx = threadIdx.x + k * BS;
+        if (idx < GQ * hd) {
           const int g = idx / hd, d = idx % hd;
-          st_coherent(m.part + ((size_t)(kvh * G + g) * m.max_split + sp) * hpart + d, o[k]);
+          float *pp = m.part + ((size_t)(kvh * GQ + g) * m.max_split + sp) * hpart;
+          st_coherent(pp + d, Ofin[k]);
+          if (d == 0) {
+            st_coherent(pp + hd, Mfin[k]);
+            st_coherent(pp + hd + 1, Lfin[k]);
+          }
         }
-      }
-      if (threadIdx.x < G) {
-        float *pp = m.part + ((size_t)(kvh * G + threadIdx.x) * m.max_split + sp) * hpart;
-        st_coherent(pp + hd, ml[threadIdx.x]);
-        st_coherent(pp + hd + 1, ml[ATT_MAX_G + threadIdx.x]);
       }
       vmem_drain();
       __syncthreads();
@@ -598,20 +911,49 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
       }
       __syncthreads();
       if (flag[0]) {
-        // log-sum-exp merge of the splits for every head of the group
-        for (int idx = threadIdx.x; idx < npairs; idx += GL3_BLOCK) {
-          const int g = idx / hd, d = idx % hd;
-          const float *base = m.part + (size_t)(kvh * G + g) * m.max_split * hpart;
+        // log-sum-exp merge of the splits: out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s
+        float *wsp = wp;  // [GQ][nsplit] weights, [GQ][nsplit] sums, [GQ] denominators
+        for (int i = threadIdx.x; i < GQ * nsplit; i += BS) {
+          const int gg = i / nsplit, s = i % nsplit;
+          const float *pp = m.part + ((size_t)(kvh * GQ + gg) * m.max_split + s) * hpart;
+          wsp[i] = ld_coherent(pp + hd);
+          wsp[GQ * nsplit + i] = ld_coherent(pp + hd + 1);
+        }
+        __syncthreads();
+        for (int gg = wave; gg < GQ; gg += WPB) {
           float M = -INFINITY;
-          for (int s = 0; s < nsplit; ++s) M = fmaxf(M, ld_coherent(base + (size_t)s * hpart + hd));
-          float Ls = 0.0f, O = 0.0f;
-          for (int s = 0; s < nsplit; ++s) {
-            const float *ps_ = base + (size_t)s * hpart;
-            float w = expf(ld_coherent(ps_ + hd) - M);
-            Ls += w * ld_coherent(ps_ + hd + 1);
-            O += w * ld_coherent(ps_ + d);
+          for (int s = lane; s < nsplit; s += GL3_WAVE) M = fmaxf(M, wsp[gg * nsplit + s]);
+          M = wave_max(M);
+          float Ls = 0.0f;
+          for (int s = lane; s < nsplit; s += GL3_WAVE) {
+            float w = (wsp[gg * nsplit + s] == -INFINITY) ? 0.0f : __expf(wsp[gg * nsplit + s] - M);
+            Ls += w * wsp[GQ * nsplit + gg * nsplit + s];
+            wsp[gg * nsplit + s] = w;
           }
-          st_coherent(m.att + (size_t)(kvh * G + g) * hd + d, O / Ls);
+          Ls = wave_sum(Ls);
+          if (lane == 0) wsp[2 * GQ * nsplit + gg] = Ls;
+        }
+        __syncthreads();
+        for (int i = 4 * threadIdx.x; i < GQ * hd; i += 4 * BS) {
+          const int gg = i / hd, dd = i % hd;  // hd % 4 == 0: the 4 values share gg
+          const float *wg = wsp + gg * nsplit;
+          const float *base = m.part + (size_t)(kvh * GQ + gg) * m.max_split * hpart;
+          float4 O = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll 4
+          for (int s = 0; s < nsplit; ++s) {
+            float4 ov = ld_coherent_f4(base, s * hpart + dd);
+            const float w = wg[s];
+            O.x += w * ov.x;
+            O.y += w * ov.y;
+            O.z += w * ov.z;
+            O.w += w * ov.w;
+          }
+          const float Ls = wsp[2 * GQ * nsplit + gg];
+          float *dst = m.att + (size_t)(kvh * GQ + gg) * hd + dd;
+          st_coherent(dst + 0, O.x / Ls);
+          st_coherent(dst + 1, O.y / Ls);
+          st_coherent(dst + 2, O.z / Ls);
+          st_coherent(dst + 3, O.w / Ls);
         }
       }
     }

@@ -213,11 +213,10 @@ static int validate_config(const gl3_config *c, int *family) {
   if (c->n_heads % c->n_kv_heads) return fail(GL3_ERR_INVALID_ARGUMENT, "n_heads %% n_kv_heads != 0");
   if (*family != FAM_QWEN3 && c->head_dim * c->n_heads != c->dim)
     return fail(GL3_ERR_INVALID_ARGUMENT, "head_dim * n_heads must equal dim for this model type");
-  if (c->head_dim % 8 || c->head_dim > 256)
-    return fail(GL3_ERR_UNSUPPORTED, "head_dim %d: must be a multiple of 8 and <= 256", c->head_dim);
   const int G = c->n_heads / c->n_kv_heads;
-  if (G > ATT_MAX_G || G * c->head_dim > 4 * GL3_BLOCK)
-    return fail(GL3_ERR_UNSUPPORTED, "GQA group %d x head_dim %d too large", G, c->head_dim);
+  if (!attention_supported(c->head_dim, G))
+    return fail(GL3_ERR_UNSUPPORTED, "head_dim %d (multiple of 8, <= 128) / GQA group %d (1, 2, 4 or 8) not supported",
+                c->head_dim, G);
   if (!(c->rms_norm_eps > 0.0f) || !(c->rope_theta > 0.0f)) return fail(GL3_ERR_INVALID_ARGUMENT, "eps/theta");
   const int fmt = ggml_to_fmt(c->weight_type);
   const int q_dim = c->n_heads * c->head_dim;
@@ -299,7 +298,8 @@ extern "C" int gl3_create(const gl3_config *cfg, gl3_plan **out) {
   m.ctx = cfg->context_length;
   m.eps = cfg->rms_norm_eps;
   m.sqrt_hd = (float)std::sqrt((double)hd);  // (float) Math.sqrt(headSize), InferenceCore.java:64
-  int ms = (2 * p->n_cu) / cfg->n_kv_heads;
+  // about one attention work item (kv head, split) per CU
+  int ms = p->n_cu / cfg->n_kv_heads;
   m.max_split = ms < 1 ? 1 : (ms > 256 ? 256 : ms);
   m.out_norm = p->out_norm;
   m.layers = p->layers_d;
@@ -316,13 +316,14 @@ extern "C" int gl3_create(const gl3_config *cfg, gl3_plan **out) {
   TRY(dev_alloc(p, &m.att, p->q_dim));
   TRY(dev_alloc(p, &m.hb, H));
   TRY(dev_alloc(p, &m.logits, cfg->vocab_size));
-  TRY(dev_alloc(p, &m.part, (size_t)cfg->n_heads * m.max_split * (hd + 2)));
+  TRY(dev_alloc(p, &m.part, (size_t)cfg->n_heads * m.max_split * (hd + 4)));
   TRY(dev_alloc(p, &m.att_ctr, (size_t)L * cfg->n_kv_heads));
   p->nbest = 2048;
   if (p->n_cu > p->nbest) p->nbest = p->n_cu;
   TRY(dev_alloc(p, &m.best, 2 * (size_t)p->nbest));
   TRY(dev_alloc(p, &m.st, 1));
   TRY(dev_alloc(p, &m.tokens_out, (size_t)cfg->context_length));
+  if (cfg->flags & GL3_FLAG_PHASE_TRACE) TRY(dev_alloc(p, &m.tstamp, (size_t)(4 + 10 * L)));
   unsigned *bar = nullptr;
   TRY(dev_alloc(p, &bar, 8 * GL3_BAR_STRIDE + 64));
   p->gb.ctr = bar;
@@ -607,13 +608,18 @@ extern "C" int gl3_prepare(gl3_plan *p) {
 
   // persistent kernel when the shape has one and the device co-schedules one workgroup per CU
   p->use_step_kernel = false;
-  if (!(c.flags & GL3_FLAG_PHASE_KERNELS) && find_step_kernel(m, &p->sk)) {
-    int dev_coop = 0;
+  if (!(c.flags & GL3_FLAG_PHASE_KERNELS) && find_step_kernel(m, p->n_cu, &p->sk)) {
+    int dev_coop = 0, max_lds = 0;
     HIP_TRY(hipDeviceGetAttribute(&dev_coop, hipDeviceAttributeCooperativeLaunch, p->device));
-    HIP_TRY(hipFuncSetAttribute(p->sk.fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)p->sk.lds_bytes));
+    HIP_TRY(hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, p->device));
+    hipFuncAttributes fa;
+    HIP_TRY(hipFuncGetAttributes(&fa, p->sk.fn));
     int per_cu = 0;
-    HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, p->sk.fn, GL3_BLOCK, p->sk.lds_bytes));
-    if (dev_coop && per_cu >= 1) {
+    if (dev_coop && fa.sharedSizeBytes + p->sk.lds_bytes <= (size_t)max_lds) {
+      HIP_TRY(hipFuncSetAttribute(p->sk.fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)p->sk.lds_bytes));
+      HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, p->sk.fn, GL3_STEP_BLOCK, p->sk.lds_bytes));
+    }
+    if (per_cu >= 1) {
       p->use_step_kernel = true;
       p->step_grid = p->n_cu;
     }
@@ -791,6 +797,19 @@ extern "C" int gl3_fill_kv_normal(gl3_plan *p, uint64_t seed, int npos) {
   return GL3_OK;
 }
 
+extern "C" int gl3_get_phase_trace(gl3_plan *p, double *us_out, int32_t max_entries, int32_t *n_out) {
+  if (!p || !us_out || !n_out) return fail(GL3_ERR_INVALID_ARGUMENT, "null argument");
+  if (!p->m.tstamp) return fail(GL3_ERR_STATE, "plan was created without GL3_FLAG_PHASE_TRACE");
+  if (!p->use_step_kernel) return fail(GL3_ERR_STATE, "the phase trace is recorded by the persistent per-token kernel only");
+  const int n = 3 + 10 * p->cfg.n_layers + 1;
+  std::vector<unsigned long long> t(n);
+  HIP_TRY(hipMemcpy(t.data(), p->m.tstamp, (size_t)n * 8, hipMemcpyDeviceToHost));
+  int k = 0;
+  for (int i = 1; i < n && k < max_entries; ++i) us_out[k++] = (double)(t[i] - t[i - 1]) * 0.01;  // 100 MHz ticks
+  *n_out = k;
+  return GL3_OK;
+}
+
 extern "C" int gl3_get_timing(gl3_plan *p, double *elapsed_ms, double *kernel_ms, int32_t *launches) {
   if (!p) return fail(GL3_ERR_INVALID_ARGUMENT, "null plan");
   if (elapsed_ms) *elapsed_ms = p->last_elapsed_ms;
@@ -880,10 +899,10 @@ extern "C" int gl3_op_gemv(int ggml_type, const void *w, int rows, int cols, con
 extern "C" int gl3_op_attention(const float *q, const uint16_t *kcache, const uint16_t *vcache, int n_heads,
                                 int n_kv_heads, int head_dim, int pos, float *out) {
   if (!q || !kcache || !vcache || !out || n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads || pos < 0 ||
-      head_dim % 8 || head_dim > 256)
+      head_dim <= 0)
     return fail(GL3_ERR_INVALID_ARGUMENT, "bad attention arguments");
   const int G = n_heads / n_kv_heads, hd = head_dim, ctx = pos + 1;
-  if (G > ATT_MAX_G || G * hd > 4 * GL3_BLOCK) return fail(GL3_ERR_UNSUPPORTED, "GQA group too large");
+  if (!attention_supported(hd, G)) return fail(GL3_ERR_UNSUPPORTED, "head_dim %d / GQA group %d not supported", hd, G);
   const int q_dim = n_heads * hd, kv_dim = n_kv_heads * hd;
   int dev = 0;
   HIP_TRY(hipGetDevice(&dev));
@@ -899,7 +918,7 @@ extern "C" int gl3_op_attention(const float *q, const uint16_t *kcache, const ui
   m.kv_dim = kv_dim;
   m.ctx = ctx;
   m.sqrt_hd = (float)std::sqrt((double)hd);
-  int ms = (2 * n_cu) / n_kv_heads;
+  int ms = n_cu / n_kv_heads;
   m.max_split = ms < 1 ? 1 : (ms > 256 ? 256 : ms);
   DevBuf layers, kc, vc, rc_, rs_, qkv, att, part, ctr, st;
   DEV_ALLOC(layers, sizeof(LayerDev));
@@ -909,7 +928,7 @@ extern "C" int gl3_op_attention(const float *q, const uint16_t *kcache, const ui
   DEV_ALLOC(rs_, (size_t)ctx * (hd / 2) * 4);
   DEV_ALLOC(qkv, (size_t)(q_dim + 2 * kv_dim) * 4);
   DEV_ALLOC(att, (size_t)q_dim * 4);
-  DEV_ALLOC(part, (size_t)n_heads * m.max_split * (hd + 2) * 4);
+  DEV_ALLOC(part, (size_t)n_heads * m.max_split * (hd + 4) * 4);
   DEV_ALLOC(ctr, (size_t)n_kv_heads * 4);
   DEV_ALLOC(st, sizeof(DecodeState));
   LayerDev L{};

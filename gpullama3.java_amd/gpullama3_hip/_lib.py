@@ -28,6 +28,7 @@ TYPE_F32, TYPE_F16, TYPE_Q8_0 = 0, 1, 8
 
 FLAG_PHASE_KERNELS = 1
 FLAG_TIMING = 2
+FLAG_PHASE_TRACE = 4
 
 GEMV_STORE, GEMV_RESIDUAL, GEMV_SWIGLU = 0, 1, 2
 
@@ -72,6 +73,7 @@ SIGNATURES = {
     "gl3_read_kv": (_I, [_P, _I, _I, _I, _U16P, _U16P]),
     "gl3_fill_kv_normal": (_I, [_P, ctypes.c_uint64, _I]),
     "gl3_get_timing": (_I, [_P, _DP, _DP, _IP]),
+    "gl3_get_phase_trace": (_I, [_P, _DP, ctypes.c_int32, _IP]),
     "gl3_destroy": (None, [_P]),
     "gl3_last_error": (ctypes.c_char_p, []),
     "gl3_device_name": (_I, [ctypes.c_char_p, _SZ]),

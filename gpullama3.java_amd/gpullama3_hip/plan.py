@@ -100,6 +100,14 @@ class HipMasterPlan:
         _ok(self.lib.gl3_get_timing(self.h, ctypes.byref(e), ctypes.byref(k), ctypes.byref(n)))
         return e.value, k.value, n.value
 
+    def phase_trace(self):
+        """Per-phase durations (us) of the last persistent-kernel step (needs FLAG_PHASE_TRACE)."""
+        out = np.zeros(16 + 10 * self.shape.n_layers, dtype=np.float64)
+        n = ctypes.c_int32()
+        _ok(self.lib.gl3_get_phase_trace(self.h, out.ctypes.data_as(ctypes.POINTER(ctypes.c_double)), out.size,
+                                         ctypes.byref(n)))
+        return out[:n.value]
+
     def reset(self):
         _ok(self.lib.gl3_reset(self.h))
 

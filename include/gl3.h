@@ -84,6 +84,7 @@ typedef enum gl3_tensor_kind {
 #define GL3_FLAG_PHASE_KERNELS 1u  /* run one kernel per phase (captured in a hipGraph) instead of
                                       the persistent per-token kernel */
 #define GL3_FLAG_TIMING 2u         /* record HIP events around every launch (gl3_get_timing) */
+#define GL3_FLAG_PHASE_TRACE 4u    /* workgroup 0 of the persistent kernel stamps every phase boundary */
 
 /* Shape of the model.  Filled by the Java host from the reference's
  * Configuration (model/Configuration.java) — head_dim is
@@ -160,6 +161,14 @@ int gl3_fill_kv_normal(gl3_plan *p, uint64_t seed, int npos);
  * GL3_FLAG_TIMING): total elapsed ms on the plan's stream, summed kernel ms, and
  * the number of kernel launches. */
 int gl3_get_timing(gl3_plan *p, double *elapsed_ms, double *kernel_ms, int32_t *launches);
+
+/* Phase trace of the last step of the persistent per-token kernel (needs
+ * GL3_FLAG_PHASE_TRACE): durations in microseconds, as seen by workgroup 0, of
+ * embedding, barrier, then per layer {QKV, barrier, attention, barrier, Wo,
+ * barrier, gate/up, barrier, down, barrier}, then the classifier.  *n_out gets
+ * the number of entries written.  No reference counterpart (the reference's
+ * TornadoVM profiler times whole task graphs: llama-tornado:131-134). */
+int gl3_get_phase_trace(gl3_plan *p, double *us_out, int32_t max_entries, int32_t *n_out);
 
 /* Replaces freeTornadoExecutionPlan (TornadoVMMasterPlan.java:200-202). */
 void gl3_destroy(gl3_plan *p);
