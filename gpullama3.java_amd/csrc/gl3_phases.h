@@ -73,7 +73,7 @@ struct ModelDev {
 // counter when it leaves a phase (before the grid barrier) and when it enters
 // the next one (after the barrier).
 __device__ __forceinline__ void trace(const ModelDev &m, int idx) {
-  if (m.tstamp && blockIdx.x == 0 && threadIdx.x == 0) m.tstamp[idx] = __builtin_amdgcn_s_memrealtime();
+  if (m.tstamp && threadIdx.x == 0) m.tstamp[(size_t)idx * gridDim.x + blockIdx.x] = __builtin_amdgcn_s_memrealtime();
 }
 
 // ------------------------------------------------------------ step control
@@ -619,62 +619,29 @@ struct GemvPhase {
 // head, split of positions); the workgroup serves the GQ query heads of the kv
 // head's GQA group, so each K/V row is read from HBM once per group.
 //
-// Inside a work item every wavefront owns positions in steps of PPW = 64/LP:
-// LP lanes read one position's K and V row with 16-byte loads (8 fp16 each),
-// hold q in registers, reduce the GQ scores over the LP lanes with DPP and keep
-// an online softmax state (max, sum, o) per lane group in registers.  The lane
-// groups of a wave are merged with shuffles, the waves through LDS, and the
-// splits of a kv head by log-sum-exp in the workgroup that finishes last.
+// Every wavefront owns positions in steps of PPW = 64/LP: LP lanes hold 8
+// dimensions each of one position's K and V row (16-byte loads), q of all GQ
+// heads in registers, reduce the GQ scores over the LP lanes with DPP and keep
+// an online softmax state (max, sum, o) per lane group in registers.  K/V
+// loads run ATT_DEPTH steps ahead in a register ring.  The lane groups of a
+// wave are merged with shuffles, the waves through LDS, and the splits of a kv
+// head by log-sum-exp in the workgroup that finishes last.
 //
-// Scores are (q . k) / sqrt(hd) (InferenceCore.java:114-121).  The same
-// workgroup applies the Qwen3 per-head RMSNorm and RoPE to q and, for the split
-// holding `pos`, to k, and appends k,v to the cache (InferenceCore.java:82-100,
-// :341-372, :472-491).
+// q (and, in the split holding `pos`, the new k and v) are read straight into
+// registers together with the RoPE table entries and the first K/V rows, so
+// the preparation costs one memory round trip: the Qwen3 per-head RMSNorm is a
+// lane-group sum, RoPE rotates pairs inside a lane (Llama, interleaved) or
+// across lanes half a head apart (NeoX).  Scores are (q . k) / sqrt(hd)
+// (InferenceCore.java:114-121); norm and RoPE follow InferenceCore.java:82-100,
+// :341-372, :472-491.
 
-#define ATT_MAX_G 8
-#define ATT_UNROLL 2
+#define ATT_DEPTH 8
 
 __device__ __forceinline__ void rope_pair(float &v0, float &v1, float c, float s) {
   float a = v0 * c - v1 * s;
   float b = v0 * s + v1 * c;
   v0 = a;
   v1 = b;
-}
-
-// Prepare `nvec` head vectors of length hd from src (coherent) into dst (LDS):
-// optional per-head RMSNorm, then RoPE at pos.  Ends with __syncthreads().
-template <int BS>
-__device__ inline void prep_heads(const ModelDev &m, const float *src, int nvec, const float *normw, int pos,
-                                  float *dst) {
-  const int hd = m.hd, half = hd / 2;
-  for (int i = 4 * threadIdx.x; i < nvec * hd; i += 4 * BS) *(float4 *)(dst + i) = ld_coherent_f4(src, i);
-  __syncthreads();
-  if (normw) {
-    // one wave per head vector: ss = sum x^2; x = w * (ss * x)   (InferenceCore.java:341-347)
-    const int wave = threadIdx.x / GL3_WAVE, lane = threadIdx.x % GL3_WAVE;
-    for (int g = wave; g < nvec; g += BS / GL3_WAVE) {
-      float ss = 0.0f;
-      for (int d = lane; d < hd; d += GL3_WAVE) ss += dst[g * hd + d] * dst[g * hd + d];
-      ss = wave_sum(ss);
-      ss /= (float)hd;
-      ss += m.eps;
-      ss = (float)(1.0 / sqrt((double)ss));
-      for (int d = lane; d < hd; d += GL3_WAVE) dst[g * hd + d] = normw[d] * (ss * dst[g * hd + d]);
-    }
-    __syncthreads();
-  }
-  const float *cr = m.rope_cos + (size_t)pos * half, *ci = m.rope_sin + (size_t)pos * half;
-  for (int t = threadIdx.x; t < nvec * half; t += BS) {
-    const int g = t / half, i = t % half;
-    int i0, i1;
-    if (m.family == FAM_LLAMA) { i0 = 2 * i; i1 = 2 * i + 1; }
-    else { i0 = i; i1 = i + half; }
-    float v0 = dst[g * hd + i0], v1 = dst[g * hd + i1];
-    rope_pair(v0, v1, cr[i], ci[i]);
-    dst[g * hd + i0] = v0;
-    dst[g * hd + i1] = v1;
-  }
-  __syncthreads();
 }
 
 // Positions per split: a multiple of the workgroup's positions per step.
@@ -684,64 +651,71 @@ __host__ __device__ __forceinline__ int att_split_len(int n, int max_split, int 
   return s < step ? step : s;
 }
 
-// LDS floats of the attention phase: q, new k/v, per-wave partials or merge weights, flag.
-__host__ __device__ __forceinline__ int att_region_floats(int hd, int G, int wpb, int max_split) {
-  const int wparts = wpb * G * (hd + 4);
-  const int merge = 2 * G * max_split + G + 8;
-  return wparts > merge ? wparts : merge;
-}
+// LDS floats of the attention phase: lane-group states o [PPB][G][hd], (m, l)
+// [PPB][G][2] and a flag, with PPB = 64 / LP lane groups per wave x wpb waves.
 __host__ __device__ __forceinline__ int att_lds_floats(int hd, int G, int wpb, int max_split) {
-  return G * hd + 2 * hd + att_region_floats(hd, G, wpb, max_split) + 16;
+  (void)max_split;
+  const int ppb = (GL3_WAVE / (hd <= 64 ? 8 : 16)) * wpb;
+  return ppb * G * (hd + 2) + 16;
 }
 
-template <int GQ>
-__device__ __forceinline__ void online_update(float (&mr)[GQ], float (&lr)[GQ], float (&o)[GQ][8], const float (&s)[GQ],
-                                              const float (&vf)[8]) {
-#pragma unroll
-  for (int g = 0; g < GQ; ++g) {
-    const float mn = fmaxf(mr[g], s[g]);
-    const float c = __expf(mr[g] - mn);
-    const float p = __expf(s[g] - mn);
-    lr[g] = lr[g] * c + p;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o[g][i] = fmaf(p, vf[i], o[g][i] * c);
-    mr[g] = mn;
-  }
+__device__ __forceinline__ void f4_to(float *dst, float4 v) {
+  dst[0] = v.x;
+  dst[1] = v.y;
+  dst[2] = v.z;
+  dst[3] = v.w;
 }
 
-// Merge (m, l, o) of lane groups `mask` apart within the wave.
-template <int GQ>
-__device__ __forceinline__ void merge_lanes(float (&mr)[GQ], float (&lr)[GQ], float (&o)[GQ][8], int mask) {
+// Qwen3 per-head RMSNorm of the 8 dims a lane holds (lane group = one head):
+// v = w * (ss * v), ss = 1/sqrt(mean(v^2) + eps)  (InferenceCore.java:341-347)
+template <int LP>
+__device__ __forceinline__ void head_norm(float (&v)[8], const float (&w)[8], int hd, float eps) {
+  float ss = 0.0f;
 #pragma unroll
-  for (int g = 0; g < GQ; ++g) {
-    const float m2 = __shfl_xor(mr[g], mask), l2 = __shfl_xor(lr[g], mask);
-    const float mn = fmaxf(mr[g], m2);
-    const float c1 = (mn == -INFINITY) ? 0.0f : __expf(mr[g] - mn);
-    const float c2 = (mn == -INFINITY) ? 0.0f : __expf(m2 - mn);
-    lr[g] = lr[g] * c1 + l2 * c2;
+  for (int i = 0; i < 8; ++i) ss += v[i] * v[i];
+  ss = group_sum<LP>(ss);
+  ss /= (float)hd;
+  ss += eps;
+  ss = (float)(1.0 / sqrt((double)ss));
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = w[i] * (ss * v[i]);
+}
+
+// RoPE of the 8 dims d0..d0+7 a lane holds.  Llama: pairs (2i, 2i+1) with
+// table entry i (c, s hold entries d0/2 .. d0/2+3).  NeoX: pairs (i, i+hd/2)
+// with entry i; the partner dims live in lane `partner` (c, s hold entries
+// (d0 mod hd/2) .. +7).  Inactive lanes (d0 >= hd) take part in the shuffle only.
+__device__ __forceinline__ void rope_lane(float (&v)[8], const float (&c)[8], const float (&s)[8], bool neox,
+                                          bool low, int partner) {
+  if (!neox) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rope_pair(v[2 * i], v[2 * i + 1], c[i], s[i]);
+  } else {
+    float o[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = __shfl(v[i], partner);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float o2 = __shfl_xor(o[g][i], mask);
-      o[g][i] = o[g][i] * c1 + o2 * c2;
+      float v0 = low ? v[i] : o[i], v1 = low ? o[i] : v[i];
+      rope_pair(v0, v1, c[i], s[i]);
+      v[i] = low ? v0 : v1;
     }
-    mr[g] = mn;
   }
 }
 
 template <int LP, int GQ, int BS>
 __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, int nblk, float *lds) {
   constexpr int WPB = BS / GL3_WAVE, PPW = GL3_WAVE / LP, PPB = PPW * WPB;
-  const int hd = m.hd, kv_dim = m.kv_dim;
+  const int hd = m.hd, half = hd / 2;
   const int n = pos + 1;
-  const int S = att_split_len(n, m.max_split, PPB * ATT_UNROLL);
+  const int S = att_split_len(n, m.max_split, PPB);
   const int nsplit = (n + S - 1) / S;
   const int items = m.n_kv * nsplit;
   const int hpart = hd + 4;
-  float *qs = lds;                 // [GQ][hd]
-  float *knew = qs + GQ * hd;      // [hd]
-  float *vnew = knew + hd;         // [hd]
-  float *wp = vnew + hd;           // per-wave partials [WPB][GQ][hd + 4], then merge weights
-  int *flag = (int *)(wp + att_region_floats(hd, GQ, WPB, m.max_split));
+  static_assert(LP == 8 || LP == 16, "lane group");
+  float *opart = lds;                     // lane-group o [PPB][GQ][hd]
+  float *mlp = opart + PPB * GQ * hd;     // lane-group (m, l) [PPB][GQ][2]
+  int *flag = (int *)(mlp + PPB * GQ * 2);
   const LayerDev &L = m.layers[layer];
   const size_t head_stride = (size_t)m.ctx * hd;
   uint16_t *kc_l = m.kc + (size_t)layer * m.n_kv * head_stride;
@@ -749,49 +723,97 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
   const int wave = threadIdx.x / GL3_WAVE, lane = threadIdx.x % GL3_WAVE;
   const int grp = lane / LP, sub = lane % LP, d0 = 8 * sub;
   const bool act = d0 < hd;
+  const bool neox = m.family != FAM_LLAMA;
+  const bool low = d0 < half;
+  const int partner = (lane - sub) + (low ? sub + half / 8 : sub - half / 8);
+  const bool qwen = m.family == FAM_QWEN3;
+  const int te = neox ? (low ? d0 : d0 - half) : d0 / 2;  // first RoPE table entry of the lane
 
   for (int item = blk; item < items; item += nblk) {
     const int kvh = item / nsplit, sp = item % nsplit;
     const int t0 = sp * S, t1 = min(n, t0 + S);
+    const bool owns_pos = (pos >= t0 && pos < t1);
     uint16_t *kh = kc_l + kvh * head_stride;
     uint16_t *vh = vc_l + kvh * head_stride;
-    // K/V rows of the first step do not depend on q: load them before preparing q
-    u32x4 kw[ATT_UNROLL], vw[ATT_UNROLL];
-    const int tb0 = t0 + wave * PPW;
+    const int tb0 = t0 + wave * PPW + grp;
+
+    // ---- one round trip: q, new k/v, RoPE entries, norm weights, first K/V rows
+    float qr[GQ][8], kn[8], vn[8], rc[8], rs[8], qw[8], kw8[8];
+    if (act) {
 #pragma unroll
-    for (int u = 0; u < ATT_UNROLL; ++u) {
-      const int t = tb0 + u * PPB + grp;
+      for (int g = 0; g < GQ; ++g) {
+        const unsigned qo = (unsigned)((kvh * GQ + g) * hd + d0);
+        f4_to(&qr[g][0], ld_coherent_f4(m.qkv, qo));
+        f4_to(&qr[g][4], ld_coherent_f4(m.qkv, qo + 4));
+      }
+      if (owns_pos) {
+        const unsigned ko = (unsigned)(m.q_dim + kvh * hd + d0), vo = ko + (unsigned)m.kv_dim;
+        f4_to(&kn[0], ld_coherent_f4(m.qkv, ko));
+        f4_to(&kn[4], ld_coherent_f4(m.qkv, ko + 4));
+        f4_to(&vn[0], ld_coherent_f4(m.qkv, vo));
+        f4_to(&vn[4], ld_coherent_f4(m.qkv, vo + 4));
+      }
+      const float *cr = m.rope_cos + (size_t)pos * half + te, *ci = m.rope_sin + (size_t)pos * half + te;
+      f4_to(&rc[0], *(const float4 *)cr);
+      f4_to(&rs[0], *(const float4 *)ci);
+      if (neox) {
+        f4_to(&rc[4], *(const float4 *)(cr + 4));
+        f4_to(&rs[4], *(const float4 *)(ci + 4));
+      }
+      if (qwen) {
+        f4_to(&qw[0], *(const float4 *)(L.q_norm + d0));
+        f4_to(&qw[4], *(const float4 *)(L.q_norm + d0 + 4));
+        f4_to(&kw8[0], *(const float4 *)(L.k_norm + d0));
+        f4_to(&kw8[4], *(const float4 *)(L.k_norm + d0 + 4));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+#pragma unroll
+        for (int g = 0; g < GQ; ++g) qr[g][i] = 0.0f;
+        kn[i] = vn[i] = rc[i] = rs[i] = qw[i] = kw8[i] = 0.0f;
+      }
+    }
+    u32x4 kr[ATT_DEPTH], vr[ATT_DEPTH];
+#pragma unroll
+    for (int u = 0; u < ATT_DEPTH; ++u) {
+      const int t = tb0 + u * PPB;
       if (act && t < t1 && t != pos) {
-        kw[u] = ld_stream(kh + (size_t)t * hd + d0);
-        vw[u] = ld_stream(vh + (size_t)t * hd + d0);
+        kr[u] = ld_stream(kh + (size_t)t * hd + d0);
+        vr[u] = ld_stream(vh + (size_t)t * hd + d0);
       } else {
-        kw[u] = u32x4{0u, 0u, 0u, 0u};
-        vw[u] = u32x4{0u, 0u, 0u, 0u};
+        kr[u] = u32x4{0u, 0u, 0u, 0u};
+        vr[u] = u32x4{0u, 0u, 0u, 0u};
       }
     }
-    prep_heads<BS>(m, m.qkv + (size_t)kvh * GQ * hd, GQ, m.family == FAM_QWEN3 ? L.q_norm : nullptr, pos, qs);
-    const bool owns_pos = (pos >= t0 && pos < t1);
+    // ---- q (and new k): per-head norm (Qwen3), RoPE at pos
+#pragma unroll
+    for (int g = 0; g < GQ; ++g) {
+      if (qwen) head_norm<LP>(qr[g], qw, hd, m.eps);
+      rope_lane(qr[g], rc, rs, neox, low, partner);
+    }
     if (owns_pos) {
-      prep_heads<BS>(m, m.qkv + m.q_dim + (size_t)kvh * hd, 1, m.family == FAM_QWEN3 ? L.k_norm : nullptr, pos,
-                     knew);
-      for (int d = 4 * threadIdx.x; d < hd; d += 4 * BS)
-        *(float4 *)(vnew + d) = ld_coherent_f4(m.qkv, m.q_dim + kv_dim + kvh * hd + d);
-      __syncthreads();
-      for (int d = threadIdx.x; d < hd; d += BS) {
-        uint16_t kh16 = f2h(knew[d]), vh16 = f2h(vnew[d]);
-        kh[(size_t)pos * hd + d] = kh16;
-        vh[(size_t)pos * hd + d] = vh16;
-        knew[d] = h2f(kh16);
-        vnew[d] = h2f(vh16);
+      if (qwen) head_norm<LP>(kn, kw8, hd, m.eps);
+      rope_lane(kn, rc, rs, neox, low, partner);
+      // fp16 cache entries at pos; the values used below are the rounded ones
+      unsigned kb[4], vb[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint16_t k0 = f2h(kn[2 * i]), k1 = f2h(kn[2 * i + 1]);
+        const uint16_t v0 = f2h(vn[2 * i]), v1 = f2h(vn[2 * i + 1]);
+        kb[i] = (unsigned)k0 | ((unsigned)k1 << 16);
+        vb[i] = (unsigned)v0 | ((unsigned)v1 << 16);
+        kn[2 * i] = h2f(k0);
+        kn[2 * i + 1] = h2f(k1);
+        vn[2 * i] = h2f(v0);
+        vn[2 * i + 1] = h2f(v1);
       }
-      __syncthreads();
+      if (wave == 0 && grp == 0 && act) {
+        *(u32x4 *)(kh + (size_t)pos * hd + d0) = u32x4{kb[0], kb[1], kb[2], kb[3]};
+        *(u32x4 *)(vh + (size_t)pos * hd + d0) = u32x4{vb[0], vb[1], vb[2], vb[3]};
+      }
     }
-    // q slice of this lane, all heads of the group
-    float qr[GQ][8];
-#pragma unroll
-    for (int g = 0; g < GQ; ++g)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) qr[g][i] = act ? qs[g * hd + d0 + i] : 0.0f;
+
     float mr[GQ], lr[GQ], o[GQ][8];
 #pragma unroll
     for (int g = 0; g < GQ; ++g) {
@@ -800,64 +822,112 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
 #pragma unroll
       for (int i = 0; i < 8; ++i) o[g][i] = 0.0f;
     }
-    for (int tb = tb0; tb < t1; tb += ATT_UNROLL * PPB) {
-      if (tb != tb0) {
+    // ---- scores and softmax, ATT_DEPTH steps per batch: all scores of the
+    //      batch first, one rescale of the running state, then the V terms.
+    //      Slot u of the register ring is reloaded ATT_DEPTH steps ahead right
+    //      after use; steps past the split's end are skipped by the wave.
+    const int wb = __builtin_amdgcn_readfirstlane(t0 + wave * PPW);  // the wave's first position
+    for (int it = 0; wb + it * ATT_DEPTH * PPB < t1; ++it) {
+      const int tb = tb0 + it * ATT_DEPTH * PPB, wt = wb + it * ATT_DEPTH * PPB;
+      float sc[ATT_DEPTH][GQ], bm[GQ];
 #pragma unroll
-        for (int u = 0; u < ATT_UNROLL; ++u) {
-          const int t = tb + u * PPB + grp;
-          if (act && t < t1 && t != pos) {
-            kw[u] = ld_stream(kh + (size_t)t * hd + d0);
-            vw[u] = ld_stream(vh + (size_t)t * hd + d0);
+      for (int g = 0; g < GQ; ++g) bm[g] = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < ATT_DEPTH; ++u) {
+#pragma unroll
+        for (int g = 0; g < GQ; ++g) sc[u][g] = -INFINITY;
+        if (wt + u * PPB < t1) {
+          const int t = tb + u * PPB;
+          float kf[8];
+          if (t == pos) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) kf[i] = kn[i];
           } else {
-            kw[u] = u32x4{0u, 0u, 0u, 0u};
-            vw[u] = u32x4{0u, 0u, 0u, 0u};
+            const unsigned ka[4] = {kr[u].x, kr[u].y, kr[u].z, kr[u].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              kf[2 * i] = h2f_lo(ka[i]);
+              kf[2 * i + 1] = h2f_hi(ka[i]);
+            }
+          }
+          const int tn = t + ATT_DEPTH * PPB;
+          if (act && tn < t1 && tn != pos) kr[u] = ld_stream(kh + (size_t)tn * hd + d0);
+#pragma unroll
+          for (int g = 0; g < GQ; ++g) {
+            float a = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) a = fmaf(qr[g][i], kf[i], a);
+            const float sv = group_sum<LP>(a) / m.sqrt_hd;
+            if (t < t1) {
+              sc[u][g] = sv;
+              bm[g] = fmaxf(bm[g], sv);
+            }
           }
         }
       }
-#pragma unroll
-      for (int u = 0; u < ATT_UNROLL; ++u) {
-        const int t = tb + u * PPB + grp;
-        float kf[8], vf[8];
-        if (t == pos && act) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) { kf[i] = knew[d0 + i]; vf[i] = vnew[d0 + i]; }
-        } else {
-          const unsigned ka[4] = {kw[u].x, kw[u].y, kw[u].z, kw[u].w}, va[4] = {vw[u].x, vw[u].y, vw[u].z, vw[u].w};
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            kf[2 * i] = h2f_lo(ka[i]); kf[2 * i + 1] = h2f_hi(ka[i]);
-            vf[2 * i] = h2f_lo(va[i]); vf[2 * i + 1] = h2f_hi(va[i]);
-          }
-        }
-        float s[GQ];
-#pragma unroll
-        for (int g = 0; g < GQ; ++g) {
-          float a = 0.0f;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) a = fmaf(qr[g][i], kf[i], a);
-          s[g] = group_sum<LP>(a) / m.sqrt_hd;
-        }
-        if (t < t1) online_update<GQ>(mr, lr, o, s, vf);
-      }
-    }
-    // merge the lane groups of the wave, then the waves of the workgroup
-#pragma unroll
-    for (int mask = LP; mask < GL3_WAVE; mask <<= 1) merge_lanes<GQ>(mr, lr, o, mask);
-    if (grp == 0 && act) {
 #pragma unroll
       for (int g = 0; g < GQ; ++g) {
-        float *dst = wp + (wave * GQ + g) * hpart;
+        const float mn = fmaxf(mr[g], bm[g]);
+        if (mn != -INFINITY) {
+          const float c = __expf(mr[g] - mn);
+          lr[g] *= c;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) dst[d0 + i] = o[g][i];
-        if (sub == 0) {
-          dst[hd] = mr[g];
-          dst[hd + 1] = lr[g];
+          for (int i = 0; i < 8; ++i) o[g][i] *= c;
+          mr[g] = mn;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < ATT_DEPTH; ++u) {
+        if (wt + u * PPB < t1) {
+          const int t = tb + u * PPB;
+          float vf[8];
+          if (t == pos) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) vf[i] = vn[i];
+          } else {
+            const unsigned va[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              vf[2 * i] = h2f_lo(va[i]);
+              vf[2 * i + 1] = h2f_hi(va[i]);
+            }
+          }
+          const int tn = t + ATT_DEPTH * PPB;
+          if (act && tn < t1 && tn != pos) vr[u] = ld_stream(vh + (size_t)tn * hd + d0);
+#pragma unroll
+          for (int g = 0; g < GQ; ++g) {
+            if (sc[u][g] != -INFINITY) {
+              const float p = __expf(sc[u][g] - mr[g]);
+              lr[g] += p;
+#pragma unroll
+              for (int i = 0; i < 8; ++i) o[g][i] = fmaf(p, vf[i], o[g][i]);
+            }
+          }
+        }
+      }
+    }
+    // ---- the PPB lane-group states of the workgroup go to LDS; thread (g, d)
+    //      pairs merge them
+    {
+      const int pi = wave * PPW + grp;
+      if (act) {
+#pragma unroll
+        for (int g = 0; g < GQ; ++g) {
+          float *dst = opart + (pi * GQ + g) * hd + d0;
+          *(float4 *)dst = make_float4(o[g][0], o[g][1], o[g][2], o[g][3]);
+          *(float4 *)(dst + 4) = make_float4(o[g][4], o[g][5], o[g][6], o[g][7]);
+        }
+      }
+      if (sub == 0) {
+#pragma unroll
+        for (int g = 0; g < GQ; ++g) {
+          mlp[(pi * GQ + g) * 2] = mr[g];
+          mlp[(pi * GQ + g) * 2 + 1] = lr[g];
         }
       }
     }
     __syncthreads();
-    // thread (g, d) pairs: combine the WPB wave partials (GQ * hd <= 4 * BS, checked by the host)
-    constexpr int PAIRS = (GQ * 128 + BS - 1) / BS;  // per-thread slots for hd <= 128
+    constexpr int PAIRS = (GQ * 128 + BS - 1) / BS;  // per-thread (g, d) slots for hd <= 128
     float Ofin[PAIRS], Mfin[PAIRS], Lfin[PAIRS];
 #pragma unroll
     for (int k = 0; k < PAIRS; ++k) {
@@ -867,16 +937,30 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
       const int idx = threadIdx.x + k * BS;
       if (idx < GQ * hd) {
         const int g = idx / hd, d = idx % hd;
-        for (int w = 0; w < WPB; ++w) Mfin[k] = fmaxf(Mfin[k], wp[(w * GQ + g) * hpart + hd]);
-        for (int w = 0; w < WPB; ++w) {
-          const float *src = wp + (w * GQ + g) * hpart;
-          const float c = (src[hd] == -INFINITY) ? 0.0f : __expf(src[hd] - Mfin[k]);
-          Lfin[k] += src[hd + 1] * c;
-          Ofin[k] += src[d] * c;
+        // all LDS reads of a pass are issued before the first use (one wave per
+        // SIMD: nothing else hides their latency)
+        float mv[PPB], lv[PPB], ov[PPB];
+#pragma unroll
+        for (int pi = 0; pi < PPB; ++pi) {
+          mv[pi] = mlp[(pi * GQ + g) * 2];
+          lv[pi] = mlp[(pi * GQ + g) * 2 + 1];
+          ov[pi] = opart[(pi * GQ + g) * hd + d];
         }
+        float M = -INFINITY;
+#pragma unroll
+        for (int pi = 0; pi < PPB; ++pi) M = fmaxf(M, mv[pi]);
+        float Ls = 0.0f, O = 0.0f;
+#pragma unroll
+        for (int pi = 0; pi < PPB; ++pi) {
+          const float w = (mv[pi] == -INFINITY) ? 0.0f : __expf(mv[pi] - M);
+          Ls = fmaf(lv[pi], w, Ls);
+          O = fmaf(ov[pi], w, O);
+        }
+        Mfin[k] = M;
+        Lfin[k] = Ls;
+        Ofin[k] = O;
       }
     }
-    __syncthreads();
     if (nsplit == 1) {
 #pragma unroll
       for (int k = 0; k < PAIRS; ++k) {
@@ -886,69 +970,86 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
           st_coherent(m.att + (size_t)(kvh * GQ + g) * hd + d, Ofin[k] / Lfin[k]);
         }
       }
-    } else {
+      __syncthreads();
+      continue;
+    }
 #pragma unroll
-      for (int k = 0; k < PAIRS; ++k) {
-        const int idx = threadIdx.x + k * BS;
-        if (idx < GQ * hd) {
-          const int g = idx / hd, d = idx % hd;
-          float *pp = m.part + ((size_t)(kvh * GQ + g) * m.max_split + sp) * hpart;
-          st_coherent(pp + d, Ofin[k]);
-          if (d == 0) {
-            st_coherent(pp + hd, Mfin[k]);
-            st_coherent(pp + hd + 1, Lfin[k]);
-          }
+    for (int k = 0; k < PAIRS; ++k) {
+      const int idx = threadIdx.x + k * BS;
+      if (idx < GQ * hd) {
+        const int g = idx / hd, d = idx % hd;
+        float *pp = m.part + ((size_t)(kvh * GQ + g) * m.max_split + sp) * hpart;
+        st_coherent(pp + d, Ofin[k]);
+        if (d == 0) {
+          st_coherent(pp + hd, Mfin[k]);
+          st_coherent(pp + hd + 1, Lfin[k]);
         }
       }
-      vmem_drain();
-      __syncthreads();
-      if (threadIdx.x == 0) {
-        unsigned *ctr = m.att_ctr + layer * m.n_kv + kvh;
-        unsigned old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int last = (old == (unsigned)(nsplit - 1));
-        flag[0] = last;
-        if (last) st_coherent_u32(ctr, 0u);
-      }
-      __syncthreads();
-      if (flag[0]) {
-        // log-sum-exp merge of the splits: out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s
-        float *wsp = wp;  // [GQ][nsplit] weights, [GQ][nsplit] sums, [GQ] denominators
-        for (int i = threadIdx.x; i < GQ * nsplit; i += BS) {
-          const int gg = i / nsplit, s = i % nsplit;
-          const float *pp = m.part + ((size_t)(kvh * GQ + gg) * m.max_split + s) * hpart;
-          wsp[i] = ld_coherent(pp + hd);
-          wsp[GQ * nsplit + i] = ld_coherent(pp + hd + 1);
-        }
-        __syncthreads();
-        for (int gg = wave; gg < GQ; gg += WPB) {
-          float M = -INFINITY;
-          for (int s = lane; s < nsplit; s += GL3_WAVE) M = fmaxf(M, wsp[gg * nsplit + s]);
-          M = wave_max(M);
-          float Ls = 0.0f;
-          for (int s = lane; s < nsplit; s += GL3_WAVE) {
-            float w = (wsp[gg * nsplit + s] == -INFINITY) ? 0.0f : __expf(wsp[gg * nsplit + s] - M);
-            Ls += w * wsp[GQ * nsplit + gg * nsplit + s];
-            wsp[gg * nsplit + s] = w;
+    }
+    vmem_drain();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      unsigned *ctr = m.att_ctr + layer * m.n_kv + kvh;
+      unsigned old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int last = (old == (unsigned)(nsplit - 1));
+      flag[0] = last;
+      if (last) st_coherent_u32(ctr, 0u);
+    }
+    __syncthreads();
+    if (flag[0]) {
+      // log-sum-exp merge of the splits: out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s.
+      // NT threads per 4 output dims, each folding splits s = q, q + NT, ... with all
+      // loads of a batch issued before any is used; then the NT partial states merge.
+      const int npos = GQ * hd / 4;  // <= BS (GQ * hd <= 4 * BS)
+      int nt = 1;                    // threads per output float4, a power of two <= 8
+      while (nt < 8 && 2 * nt * npos <= BS) nt *= 2;
+      const int pidx = threadIdx.x / nt, q = threadIdx.x % nt;
+      if (pidx < npos) {
+        const int gg = (4 * pidx) / hd, dd = (4 * pidx) % hd;
+        const float *base = m.part + (size_t)(kvh * GQ + gg) * m.max_split * hpart;
+        float M = -INFINITY, Ls = 0.0f;
+        float4 O = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int s0 = q; s0 < nsplit; s0 += 8 * nt) {
+          float4 hv[8], ov[8];
+#pragma unroll
+          for (int b = 0; b < 8; ++b) {
+            const int s = s0 + b * nt;
+            if (s < nsplit) {
+              hv[b] = ld_coherent_f4(base, (unsigned)(s * hpart + hd));
+              ov[b] = ld_coherent_f4(base, (unsigned)(s * hpart + dd));
+            }
           }
-          Ls = wave_sum(Ls);
-          if (lane == 0) wsp[2 * GQ * nsplit + gg] = Ls;
-        }
-        __syncthreads();
-        for (int i = 4 * threadIdx.x; i < GQ * hd; i += 4 * BS) {
-          const int gg = i / hd, dd = i % hd;  // hd % 4 == 0: the 4 values share gg
-          const float *wg = wsp + gg * nsplit;
-          const float *base = m.part + (size_t)(kvh * GQ + gg) * m.max_split * hpart;
-          float4 O = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll 4
-          for (int s = 0; s < nsplit; ++s) {
-            float4 ov = ld_coherent_f4(base, s * hpart + dd);
-            const float w = wg[s];
-            O.x += w * ov.x;
-            O.y += w * ov.y;
-            O.z += w * ov.z;
-            O.w += w * ov.w;
+#pragma unroll
+          for (int b = 0; b < 8; ++b) {
+            const int s = s0 + b * nt;
+            if (s < nsplit && hv[b].x != -INFINITY) {
+              const float mn = fmaxf(M, hv[b].x);
+              const float c1 = __expf(M - mn), c2 = __expf(hv[b].x - mn);
+              Ls = Ls * c1 + hv[b].y * c2;
+              O.x = O.x * c1 + ov[b].x * c2;
+              O.y = O.y * c1 + ov[b].y * c2;
+              O.z = O.z * c1 + ov[b].z * c2;
+              O.w = O.w * c1 + ov[b].w * c2;
+              M = mn;
+            }
           }
-          const float Ls = wsp[2 * GQ * nsplit + gg];
+        }
+        // merge the nt lanes of this output (adjacent lanes)
+        for (int msk = 1; msk < nt; msk <<= 1) {
+          const float M2 = __shfl_xor(M, msk), L2 = __shfl_xor(Ls, msk);
+          const float o2x = __shfl_xor(O.x, msk), o2y = __shfl_xor(O.y, msk), o2z = __shfl_xor(O.z, msk),
+                      o2w = __shfl_xor(O.w, msk);
+          const float mn = fmaxf(M, M2);
+          const float c1 = (mn == -INFINITY) ? 0.0f : __expf(M - mn);
+          const float c2 = (mn == -INFINITY) ? 0.0f : __expf(M2 - mn);
+          Ls = Ls * c1 + L2 * c2;
+          O.x = O.x * c1 + o2x * c2;
+          O.y = O.y * c1 + o2y * c2;
+          O.z = O.z * c1 + o2z * c2;
+          O.w = O.w * c1 + o2w * c2;
+          M = mn;
+        }
+        if (q == 0) {
           float *dst = m.att + (size_t)(kvh * GQ + gg) * hd + dd;
           st_coherent(dst + 0, O.x / Ls);
           st_coherent(dst + 1, O.y / Ls);

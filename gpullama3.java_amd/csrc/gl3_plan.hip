@@ -323,7 +323,7 @@ extern "C" int gl3_create(const gl3_config *cfg, gl3_plan **out) {
   TRY(dev_alloc(p, &m.best, 2 * (size_t)p->nbest));
   TRY(dev_alloc(p, &m.st, 1));
   TRY(dev_alloc(p, &m.tokens_out, (size_t)cfg->context_length));
-  if (cfg->flags & GL3_FLAG_PHASE_TRACE) TRY(dev_alloc(p, &m.tstamp, (size_t)(4 + 10 * L)));
+  if (cfg->flags & GL3_FLAG_PHASE_TRACE) TRY(dev_alloc(p, &m.tstamp, (size_t)(4 + 10 * L) * p->n_cu));
   unsigned *bar = nullptr;
   TRY(dev_alloc(p, &bar, 8 * GL3_BAR_STRIDE + 64));
   p->gb.ctr = bar;
@@ -797,16 +797,41 @@ extern "C" int gl3_fill_kv_normal(gl3_plan *p, uint64_t seed, int npos) {
   return GL3_OK;
 }
 
-extern "C" int gl3_get_phase_trace(gl3_plan *p, double *us_out, int32_t max_entries, int32_t *n_out) {
-  if (!p || !us_out || !n_out) return fail(GL3_ERR_INVALID_ARGUMENT, "null argument");
+static int trace_stamps(gl3_plan *p, std::vector<unsigned long long> &t, int *n_stamps, int *n_blocks) {
   if (!p->m.tstamp) return fail(GL3_ERR_STATE, "plan was created without GL3_FLAG_PHASE_TRACE");
   if (!p->use_step_kernel) return fail(GL3_ERR_STATE, "the phase trace is recorded by the persistent per-token kernel only");
-  const int n = 3 + 10 * p->cfg.n_layers + 1;
-  std::vector<unsigned long long> t(n);
-  HIP_TRY(hipMemcpy(t.data(), p->m.tstamp, (size_t)n * 8, hipMemcpyDeviceToHost));
+  *n_stamps = 3 + 10 * p->cfg.n_layers + 1;
+  *n_blocks = p->step_grid;
+  t.resize((size_t)*n_stamps * *n_blocks);
+  HIP_TRY(hipMemcpy(t.data(), p->m.tstamp, t.size() * 8, hipMemcpyDeviceToHost));
+  return GL3_OK;
+}
+
+extern "C" int gl3_get_phase_trace(gl3_plan *p, double *us_out, int32_t max_entries, int32_t *n_out) {
+  if (!p || !us_out || !n_out) return fail(GL3_ERR_INVALID_ARGUMENT, "null argument");
+  std::vector<unsigned long long> t;
+  int n = 0, nb = 0;
+  int rc = trace_stamps(p, t, &n, &nb);
+  if (rc) return rc;
   int k = 0;
-  for (int i = 1; i < n && k < max_entries; ++i) us_out[k++] = (double)(t[i] - t[i - 1]) * 0.01;  // 100 MHz ticks
+  for (int i = 1; i < n && k < max_entries; ++i)
+    us_out[k++] = (double)(t[(size_t)i * nb] - t[(size_t)(i - 1) * nb]) * 0.01;  // 100 MHz ticks, workgroup 0
   *n_out = k;
+  return GL3_OK;
+}
+
+extern "C" int gl3_get_phase_stamps(gl3_plan *p, uint64_t *out, int64_t max_entries, int32_t *n_stamps,
+                                    int32_t *n_workgroups) {
+  if (!p || !out || !n_stamps || !n_workgroups) return fail(GL3_ERR_INVALID_ARGUMENT, "null argument");
+  std::vector<unsigned long long> t;
+  int n = 0, nb = 0;
+  int rc = trace_stamps(p, t, &n, &nb);
+  if (rc) return rc;
+  if ((int64_t)t.size() > max_entries) return fail(GL3_ERR_INVALID_ARGUMENT, "output holds %lld entries, %zu needed",
+                                                   (long long)max_entries, t.size());
+  for (size_t i = 0; i < t.size(); ++i) out[i] = t[i];
+  *n_stamps = n;
+  *n_workgroups = nb;
   return GL3_OK;
 }
 

@@ -74,6 +74,7 @@ SIGNATURES = {
     "gl3_fill_kv_normal": (_I, [_P, ctypes.c_uint64, _I]),
     "gl3_get_timing": (_I, [_P, _DP, _DP, _IP]),
     "gl3_get_phase_trace": (_I, [_P, _DP, ctypes.c_int32, _IP]),
+    "gl3_get_phase_stamps": (_I, [_P, ctypes.POINTER(ctypes.c_uint64), ctypes.c_int64, _IP, _IP]),
     "gl3_destroy": (None, [_P]),
     "gl3_last_error": (ctypes.c_char_p, []),
     "gl3_device_name": (_I, [ctypes.c_char_p, _SZ]),

@@ -108,6 +108,16 @@ class HipMasterPlan:
                                          ctypes.byref(n)))
         return out[:n.value]
 
+    def phase_stamps(self):
+        """Raw 100 MHz stamps [boundary][workgroup] of the last persistent-kernel step (needs FLAG_PHASE_TRACE)."""
+        n_b = 4 + 10 * self.shape.n_layers
+        out = np.zeros(n_b * 4096, dtype=np.uint64)
+        ns = ctypes.c_int32()
+        nw = ctypes.c_int32()
+        _ok(self.lib.gl3_get_phase_stamps(self.h, out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64)), out.size,
+                                          ctypes.byref(ns), ctypes.byref(nw)))
+        return out[:ns.value * nw.value].reshape(ns.value, nw.value)
+
     def reset(self):
         _ok(self.lib.gl3_reset(self.h))
 

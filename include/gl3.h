@@ -170,6 +170,12 @@ int gl3_get_timing(gl3_plan *p, double *elapsed_ms, double *kernel_ms, int32_t *
  * TornadoVM profiler times whole task graphs: llama-tornado:131-134). */
 int gl3_get_phase_trace(gl3_plan *p, double *us_out, int32_t max_entries, int32_t *n_out);
 
+/* Raw phase-boundary stamps of the last persistent-kernel step for every
+ * workgroup: out[i * n_workgroups + w] = s_memrealtime (100 MHz) of workgroup
+ * w at boundary i (same boundaries as gl3_get_phase_trace, with the step's
+ * start at i = 0).  Needs GL3_FLAG_PHASE_TRACE.  No reference counterpart. */
+int gl3_get_phase_stamps(gl3_plan *p, uint64_t *out, int64_t max_entries, int32_t *n_stamps, int32_t *n_workgroups);
+
 /* Replaces freeTornadoExecutionPlan (TornadoVMMasterPlan.java:200-202). */
 void gl3_destroy(gl3_plan *p);
 
