@@ -68,7 +68,7 @@ def cpu_baseline(shape, tensors, seconds=15.0):
     m.reset()
     n, t0 = 0, time.perf_counter()
     tok = 1
-    while time.perf_counter() - t0 < seconds and n < 64:
+    while time.perf_counter() - t0 < seconds and n < min(1024, shape.context_length):
         lg = m.forward(tok, n)
         tok = int(np.argmax(lg))
         n += 1
@@ -77,6 +77,37 @@ def cpu_baseline(shape, tensors, seconds=15.0):
     return {"value": n / dt, "unit": "tok/s", "cores": threads, "kind": "port",
             "sample": f"{n} greedy decode steps at positions 0-{n - 1} of the same model, oracle (C, OpenMP, "
                       f"AVX2 8-lane dots), {dt:.1f} s"}
+
+
+def copy_calibration(n_floats=256 << 20, reps=3):
+    """A plain elementwise copy kernel of known size (reads and writes 4 * n_floats
+    bytes per dispatch), run under rocprofv3 --pmc to scale FETCH_SIZE/WRITE_SIZE."""
+    import torch
+    a = torch.ones(n_floats, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        torch.mul(a, 1.0, out=b)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_kernel": "torch.mul(a, 1.0, out=b) float32", "bytes_read_per_dispatch": 4 * n_floats,
+                      "bytes_written_per_dispatch": 4 * n_floats, "dispatches": reps}), flush=True)
+
+
+def measured_traffic(cfg_key):
+    """HBM bytes per launch of the decode kernel from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration), or None."""
+    path = os.path.join(ROOT, "profiles", f"traffic_decode_step_{cfg_key}.txt")
+    if not os.path.exists(path):
+        return None
+    vals = {}
+    with open(path) as f:
+        for line in f:
+            if ":" in line and not line.startswith("#"):
+                k, v = line.split(":", 1)
+                vals[k.strip()] = v.strip()
+    try:
+        return int(float(vals["fetch_bytes_per_launch"]) + float(vals["write_bytes_per_launch"]))
+    except (KeyError, ValueError):
+        return None
 
 
 def main():
@@ -88,7 +119,12 @@ def main():
     ap.add_argument("--schedule", default="persistent", choices=["persistent", "graph"])
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only the plain copy kernel used to calibrate rocprofv3 byte counters")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this decode path has no multi-GPU mode (--gpus {args.gpus} refused)",
               file=sys.stderr)
@@ -167,7 +203,7 @@ def main():
         "achieved_hbm_gbs": round(achieved, 1),
         "hbm_fraction": round(achieved / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.config) if args.schedule == "persistent" else None,
                      "kernel": kernel, "bytes_per_launch": int(avg_bytes),
                      "avg_launch_ms": round(avg_kernel_s * 1e3, 4)},
         "cpu_baseline": cpu,

@@ -84,7 +84,7 @@ typedef enum gl3_tensor_kind {
 #define GL3_FLAG_PHASE_KERNELS 1u  /* run one kernel per phase (captured in a hipGraph) instead of
                                       the persistent per-token kernel */
 #define GL3_FLAG_TIMING 2u         /* record HIP events around every launch (gl3_get_timing) */
-#define GL3_FLAG_PHASE_TRACE 4u    /* workgroup 0 of the persistent kernel stamps every phase boundary */
+#define GL3_FLAG_PHASE_TRACE 4u    /* every workgroup of the persistent kernel stamps every phase boundary */
 
 /* Shape of the model.  Filled by the Java host from the reference's
  * Configuration (model/Configuration.java) — head_dim is

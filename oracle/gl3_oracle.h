@@ -14,6 +14,15 @@
  * Tensor memory is borrowed, in the GGUF on-disk encodings the reference reads
  * through its mmap: F32 = float[], F16 = IEEE binary16[], Q8_0 = 34-byte blocks
  * {fp16 scale, int8 q[32]} (GGMLType.java:13).
+ *
+ * Pins (tests/test_oracle.py): exhaustive fp16 decode and Q8_0 dequant,
+ * fp64 brute force and closed forms for GEMV, RMSNorm, RoPE, softmax, argmax
+ * and attention, and fp64 golden fixtures of tiny models of every family.
+ * Parity unpinned: the exact reduceLanes(ADD) order of the Java Vector API
+ * dots (Q8_0FloatTensor.java:119, FP16FloatTensor.java:103; a fixed 8-lane
+ * order is used here) and the last-ulp behaviour of Math.exp/cos/sin/pow (C's
+ * double versions are used); the reference JVM cannot run here, so these are
+ * bounded only by the parity tolerance.
  */
 #ifndef GL3_ORACLE_H
 #define GL3_ORACLE_H

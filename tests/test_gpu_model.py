@@ -1,7 +1,7 @@
 """End-to-end parity of the decode step against the oracle, through the C ABI.
 
 Two bars: against the oracle with the test aid kv_fp16 (same fp16 KV rounding
-as the device) logits agree to 1e-4 of their std; against the oracle with the
+as the device) logits agree to 2e-3 of their std; against the oracle with the
 reference's own fp32 KV cache they agree within the 2e-2 * std tolerance and
 greedy tokens match wherever the top-2 margin exceeds it.  Both schedules (the
 persistent per-token kernel and the per-phase hipGraph) are checked.
