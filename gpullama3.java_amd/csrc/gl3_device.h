@@ -71,6 +71,21 @@ __device__ __forceinline__ void vmem_drain() { asm volatile("s_waitcnt vmcnt(0)"
 // Streaming (read-once) 16-byte load of weights / KV.
 __device__ __forceinline__ u32x4 ld_stream(const void *p) { return __builtin_nontemporal_load((const u32x4 *)p); }
 
+// ------------------------------------------------------------ lane / wave ids
+// Lane and wave indices as values the compiler cannot hoist out of the layer
+// loop of the persistent kernel: address arithmetic derived from them stays in
+// the phase that uses it instead of holding registers for the whole kernel.
+__device__ __forceinline__ int lane_id() {
+  int l = (int)(threadIdx.x % GL3_WAVE);
+  asm volatile("" : "+v"(l));
+  return l;
+}
+__device__ __forceinline__ int wave_id() {
+  int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / GL3_WAVE));
+  asm volatile("" : "+s"(w));
+  return w;
+}
+
 // ------------------------------------------------------------ reductions
 
 template <int CTRL>

@@ -217,39 +217,42 @@ __global__ __launch_bounds__(GL3_STEP_BLOCK, 1) void decode_step_kernel(ModelDev
   phase_embed(m, si.token, blk, nblk);
   trace(m, tk++);
   grid_arrive(gb);
-  SH::QKV::prefetch(m.layers[0].qkv, rows_qkv, blk, nblk);
+  // layer descriptors are loaded where they are used (scalar loads), so only
+  // the current phase's matrix occupies registers
+  const cLayerDev *layers = (const cLayerDev *)m.layers;
+  SH::QKV::prefetch(ld_mat(&layers[0].qkv), rows_qkv, blk, nblk);
   if (!grid_wait(gb, ++epoch)) return;
   trace(m, tk++);
   if (blk == 0) advance_step(m, si);
   for (int l = 0; l < m.n_layers; ++l) {
-    const LayerDev &L = m.layers[l];
-    SH::QKV::run(L.qkv, rows_qkv, m.x, L.attn_norm, m.eps, m.qkv, nullptr, blk, nblk, lds, true);
+    const cLayerDev *L = layers + l;
+    SH::QKV::run(ld_mat(&L->qkv), rows_qkv, m.x, L->attn_norm, m.eps, m.qkv, nullptr, blk, nblk, lds, true);
     trace(m, tk++);
     grid_arrive(gb);
-    SH::WO::prefetch(L.wo, SH::dim, blk, nblk);
+    SH::WO::prefetch(ld_mat(&L->wo), SH::dim, blk, nblk);
     if (!grid_wait(gb, ++epoch)) return;
     trace(m, tk++);
     phase_attention<SH::LP, SH::gqa, SH::BS>(m, l, si.pos, blk, nblk, lds);
     trace(m, tk++);
     if (!grid_barrier(gb, ++epoch)) return;
     trace(m, tk++);
-    SH::WO::run(L.wo, SH::dim, m.att, nullptr, m.eps, m.x, nullptr, blk, nblk, lds, true);
+    SH::WO::run(ld_mat(&L->wo), SH::dim, m.att, nullptr, m.eps, m.x, nullptr, blk, nblk, lds, true);
     trace(m, tk++);
     grid_arrive(gb);
-    SH::GU::prefetch(L.gu, SH::hidden, blk, nblk);
+    SH::GU::prefetch(ld_mat(&L->gu), SH::hidden, blk, nblk);
     if (!grid_wait(gb, ++epoch)) return;
     trace(m, tk++);
-    SH::GU::run(L.gu, SH::hidden, m.x, L.ffn_norm, m.eps, m.hb, nullptr, blk, nblk, lds, true);
+    SH::GU::run(ld_mat(&L->gu), SH::hidden, m.x, L->ffn_norm, m.eps, m.hb, nullptr, blk, nblk, lds, true);
     trace(m, tk++);
     grid_arrive(gb);
-    SH::DOWN::prefetch(L.down, SH::dim, blk, nblk);
+    SH::DOWN::prefetch(ld_mat(&L->down), SH::dim, blk, nblk);
     if (!grid_wait(gb, ++epoch)) return;
     trace(m, tk++);
-    SH::DOWN::run(L.down, SH::dim, m.hb, nullptr, m.eps, m.x, nullptr, blk, nblk, lds, true);
+    SH::DOWN::run(ld_mat(&L->down), SH::dim, m.hb, nullptr, m.eps, m.x, nullptr, blk, nblk, lds, true);
     trace(m, tk++);
     grid_arrive(gb);
     if (l + 1 < m.n_layers)
-      SH::QKV::prefetch(m.layers[l + 1].qkv, rows_qkv, blk, nblk);
+      SH::QKV::prefetch(ld_mat(&layers[l + 1].qkv), rows_qkv, blk, nblk);
     else
       SH::CLS::prefetch(m.cls, m.vocab, blk, nblk);
     if (!grid_wait(gb, ++epoch)) return;

@@ -34,6 +34,33 @@ struct LayerDev {
   const float *attn_norm, *ffn_norm, *q_norm, *k_norm;
 };
 
+// Layer descriptors are read through the constant address space: they are
+// written by the host only, so the loads are scalar and the matrix pointers
+// land in SGPRs (buffer descriptors built from them stay uniform).
+typedef __attribute__((address_space(4))) const Mat cMat;
+typedef __attribute__((address_space(4))) const LayerDev cLayerDev;
+__device__ __forceinline__ Mat ld_mat(const cMat *p) {
+  Mat r;
+  r.q = p->q;
+  r.s = p->s;
+  r.rows = p->rows;
+  r.cols = p->cols;
+  return r;
+}
+__device__ __forceinline__ LayerDev ld_layer(const LayerDev *layers, int l) {
+  const cLayerDev *p = (const cLayerDev *)(layers + l);
+  LayerDev r;
+  r.qkv = ld_mat(&p->qkv);
+  r.wo = ld_mat(&p->wo);
+  r.gu = ld_mat(&p->gu);
+  r.down = ld_mat(&p->down);
+  r.attn_norm = p->attn_norm;
+  r.ffn_norm = p->ffn_norm;
+  r.q_norm = p->q_norm;
+  r.k_norm = p->k_norm;
+  return r;
+}
+
 // Per-step control block in device memory.
 struct DecodeState {
   int pos;        // position of the token being forwarded
@@ -332,12 +359,11 @@ struct GemvPhase {
     const int n = items(out_rows);
     return blk < n ? (n - 1 - blk) / nblk + 1 : 0;
   }
-  static __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x / GL3_WAVE); }
 
   // Issues the loads of slot-load u (the workgroup's item u / PASSES, pass u % PASSES) into ring slot S.
   template <int S>
   static __device__ __forceinline__ void issue(const Mat &W, int out_rows, int u, int blk, int nblk) {
-    const int wave = wave_id(), lane = threadIdx.x % GL3_WAVE;
+    const int wave = wave_id(), lane = lane_id();
     const int ks = wave % KS, rg = wave / KS;
     const int K = W.cols;
     const int item = blk + (u / PASSES) * nblk, pass = PASSES > 1 ? u % PASSES : 0;
@@ -401,7 +427,7 @@ struct GemvPhase {
   // acc[r][p] += the lane's part of the dot products held in slot S (pass `pass` of the item)
   template <int S>
   static __device__ __forceinline__ void dot_slot(const XSlice &xr, int pass, float (&acc)[NR][NP]) {
-    const int wave = wave_id(), lane = threadIdx.x % GL3_WAVE;
+    const int wave = wave_id(), lane = lane_id();
     const u32x4 *rw = ring_w<S, WCH>() + wave * SC * GL3_WAVE + lane;
     const uint8_t *rs = (const uint8_t *)(ring_s<S, SDW>() + wave * SC * 16);
     const int j0 = pass * JP;
@@ -443,7 +469,7 @@ struct GemvPhase {
   // Reduces and combines the K-split partials of the workgroup's i-th item;
   // the row values go to obuf[i * ROWS_PER_ITEM + row in item].
   static __device__ __forceinline__ void finish_item(int i, float (&acc)[NR][NP], float *kpart, float *obuf) {
-    const int wave = wave_id(), lane = threadIdx.x % GL3_WAVE;
+    const int wave = wave_id(), lane = lane_id();
     const int ks = wave % KS, rg = wave / KS;
 #pragma unroll
     for (int r = 0; r < NR; ++r)
@@ -530,7 +556,7 @@ struct GemvPhase {
     const int nu = nli * PASSES;
     if (!prefetched) prefetch(W, out_rows, blk, nblk);
 
-    const int wave = wave_id(), lane = threadIdx.x % GL3_WAVE;
+    const int wave = wave_id(), lane = lane_id();
     const int ks = wave % KS;
     XSlice xr;
     xr.lds = xs;
@@ -635,7 +661,7 @@ struct GemvPhase {
 // (InferenceCore.java:114-121); norm and RoPE follow InferenceCore.java:82-100,
 // :341-372, :472-491.
 
-#define ATT_DEPTH 8
+#define ATT_DEPTH 4
 
 __device__ __forceinline__ void rope_pair(float &v0, float &v1, float c, float s) {
   float a = v0 * c - v1 * s;
@@ -716,11 +742,11 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
   float *opart = lds;                     // lane-group o [PPB][GQ][hd]
   float *mlp = opart + PPB * GQ * hd;     // lane-group (m, l) [PPB][GQ][2]
   int *flag = (int *)(mlp + PPB * GQ * 2);
-  const LayerDev &L = m.layers[layer];
+  const LayerDev L = ld_layer(m.layers, layer);
   const size_t head_stride = (size_t)m.ctx * hd;
   uint16_t *kc_l = m.kc + (size_t)layer * m.n_kv * head_stride;
   uint16_t *vc_l = m.vc + (size_t)layer * m.n_kv * head_stride;
-  const int wave = threadIdx.x / GL3_WAVE, lane = threadIdx.x % GL3_WAVE;
+  const int wave = wave_id(), lane = lane_id();
   const int grp = lane / LP, sub = lane % LP, d0 = 8 * sub;
   const bool act = d0 < hd;
   const bool neox = m.family != FAM_LLAMA;
@@ -927,7 +953,9 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
       }
     }
     __syncthreads();
-    constexpr int PAIRS = (GQ * 128 + BS - 1) / BS;  // per-thread (g, d) slots for hd <= 128
+    constexpr int PAIRS = (GQ * LP * 8 + BS - 1) / BS;  // per-thread (g, d) slots (hd <= 8 * LP)
+    constexpr int CB = 8;                                 // partials read per batch
+    static_assert(PPB % CB == 0, "lane-group partials per batch");
     float Ofin[PAIRS], Mfin[PAIRS], Lfin[PAIRS];
 #pragma unroll
     for (int k = 0; k < PAIRS; ++k) {
@@ -937,24 +965,31 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
       const int idx = threadIdx.x + k * BS;
       if (idx < GQ * hd) {
         const int g = idx / hd, d = idx % hd;
-        // all LDS reads of a pass are issued before the first use (one wave per
+        // LDS reads are issued CB at a time before their first use (one wave per
         // SIMD: nothing else hides their latency)
-        float mv[PPB], lv[PPB], ov[PPB];
-#pragma unroll
-        for (int pi = 0; pi < PPB; ++pi) {
-          mv[pi] = mlp[(pi * GQ + g) * 2];
-          lv[pi] = mlp[(pi * GQ + g) * 2 + 1];
-          ov[pi] = opart[(pi * GQ + g) * hd + d];
-        }
         float M = -INFINITY;
+        for (int p0 = 0; p0 < PPB; p0 += CB) {
+          float mv[CB];
 #pragma unroll
-        for (int pi = 0; pi < PPB; ++pi) M = fmaxf(M, mv[pi]);
+          for (int c = 0; c < CB; ++c) mv[c] = mlp[((p0 + c) * GQ + g) * 2];
+#pragma unroll
+          for (int c = 0; c < CB; ++c) M = fmaxf(M, mv[c]);
+        }
         float Ls = 0.0f, O = 0.0f;
+        for (int p0 = 0; p0 < PPB; p0 += CB) {
+          float mv[CB], lv[CB], ov[CB];
 #pragma unroll
-        for (int pi = 0; pi < PPB; ++pi) {
-          const float w = (mv[pi] == -INFINITY) ? 0.0f : __expf(mv[pi] - M);
-          Ls = fmaf(lv[pi], w, Ls);
-          O = fmaf(ov[pi], w, O);
+          for (int c = 0; c < CB; ++c) {
+            mv[c] = mlp[((p0 + c) * GQ + g) * 2];
+            lv[c] = mlp[((p0 + c) * GQ + g) * 2 + 1];
+            ov[c] = opart[((p0 + c) * GQ + g) * hd + d];
+          }
+#pragma unroll
+          for (int c = 0; c < CB; ++c) {
+            const float w = (mv[c] == -INFINITY) ? 0.0f : __expf(mv[c] - M);
+            Ls = fmaf(lv[c], w, Ls);
+            O = fmaf(ov[c], w, O);
+          }
         }
         Mfin[k] = M;
         Lfin[k] = Ls;
