@@ -111,12 +111,12 @@ __global__ __launch_bounds__(GL3_BLOCK) void embed_kernel(ModelDev m) {
   phase_embed(m, si.token, blockIdx.x, gridDim.x);
 }
 
-template <int LP, int GQ>
+template <int HD, int GQ>
 __global__ __launch_bounds__(GL3_STEP_BLOCK) void attention_kernel(ModelDev m, int layer) {
   extern __shared__ float lds[];
   __shared__ int si_lds[8];
   StepInfo si = read_step(m, si_lds);
-  phase_attention<LP, GQ, GL3_STEP_BLOCK>(m, layer, si.pos, blockIdx.x, gridDim.x, lds);
+  phase_attention<HD, GQ, GL3_STEP_BLOCK>(m, layer, si.pos, blockIdx.x, gridDim.x, lds);
 }
 
 // Last kernel of a step: records the previous token and advances the control block.
@@ -137,8 +137,6 @@ size_t attention_lds_bytes(int hd, int G, int max_split) {
   return (size_t)att_lds_floats(hd, G, GL3_STEP_BLOCK / GL3_WAVE, max_split) * sizeof(float);
 }
 
-// lanes per KV position: 8 for head_dim <= 64, 16 for head_dim <= 128
-static int att_lp(int hd) { return hd <= 64 ? 8 : 16; }
 
 hipError_t launch_embed(const ModelDev &m, hipStream_t s) {
   int grid = (m.dim + GL3_BLOCK - 1) / GL3_BLOCK;
@@ -147,19 +145,22 @@ hipError_t launch_embed(const ModelDev &m, hipStream_t s) {
 }
 hipError_t launch_attention(const ModelDev &m, int layer, hipStream_t s) {
   const int grid = m.n_kv * m.max_split;
-  const int G = m.n_heads / m.n_kv, lp = att_lp(m.hd);
+  const int G = m.n_heads / m.n_kv;
   const size_t lds = attention_lds_bytes(m.hd, G, m.max_split);
-#define GL3_ATT(LP_, G_)                                                                                        \
-  if (lp == LP_ && G == G_) {                                                                                   \
-    hipLaunchKernelGGL((attention_kernel<LP_, G_>), dim3(grid), dim3(GL3_STEP_BLOCK), lds, s, m, layer);        \
+#define GL3_ATT(HD_, G_)                                                                                        \
+  if (m.hd == HD_ && G == G_) {                                                                                 \
+    hipLaunchKernelGGL((attention_kernel<HD_, G_>), dim3(grid), dim3(GL3_STEP_BLOCK), lds, s, m, layer);        \
     return hipGetLastError();                                                                                   \
   }
-  GL3_ATT(8, 1) GL3_ATT(8, 2) GL3_ATT(8, 4) GL3_ATT(8, 8)
-  GL3_ATT(16, 1) GL3_ATT(16, 2) GL3_ATT(16, 4) GL3_ATT(16, 8)
+  GL3_ATT(64, 1) GL3_ATT(64, 2) GL3_ATT(64, 4) GL3_ATT(64, 8)
+  GL3_ATT(96, 1) GL3_ATT(96, 2) GL3_ATT(96, 4) GL3_ATT(96, 8)
+  GL3_ATT(128, 1) GL3_ATT(128, 2) GL3_ATT(128, 4) GL3_ATT(128, 8)
 #undef GL3_ATT
   return hipErrorInvalidValue;
 }
-bool attention_supported(int hd, int G) { return hd % 8 == 0 && hd <= 128 && (G == 1 || G == 2 || G == 4 || G == 8) && G * hd <= 4 * GL3_STEP_BLOCK; }
+bool attention_supported(int hd, int G) {
+  return (hd == 64 || hd == 96 || hd == 128) && (G == 1 || G == 2 || G == 4 || G == 8);
+}
 hipError_t launch_advance(const ModelDev &m, hipStream_t s) {
   hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(GL3_BLOCK), 0, s, m);
   return hipGetLastError();
@@ -185,7 +186,6 @@ template <int FMT_, int DIM, int QD, int KVD, int HID, int HD, int G, int SC, in
 struct Shape {
   static constexpr int fmt = FMT_, dim = DIM, q_dim = QD, kv_dim = KVD, hidden = HID, hd = HD, gqa = G;
   static constexpr int BS = GL3_STEP_BLOCK;
-  static constexpr int LP = HD <= 64 ? 8 : 16;
   typedef GemvPhase<FMT_, TQKV::KC, TQKV::KS, TQKV::NR, MODE_STORE, BS, SC, DEPTH> QKV;
   typedef GemvPhase<FMT_, TWO::KC, TWO::KS, TWO::NR, MODE_RESIDUAL, BS, SC, DEPTH> WO;
   typedef GemvPhase<FMT_, TGU::KC, TGU::KS, TGU::NR, MODE_SWIGLU, BS, SC, DEPTH> GU;
@@ -204,7 +204,7 @@ typedef Shape<FMT_Q8,  4096, 4096, 1024, 14336, 128, 4, 8, 3, Tile<4, 1, 2>, Til
 // down), classifier, with a grid barrier between dependent phases.  The first
 // weight tiles of each GEMV phase are requested before the barrier that
 // precedes it (weights do not depend on it), so their HBM latency overlaps
-// the barrier and, for Wo, the attention phase.
+// the barrier.
 template <class SH>
 __global__ __launch_bounds__(GL3_STEP_BLOCK, 1) void decode_step_kernel(ModelDev m, GridBarrier gb, unsigned epoch) {
   extern __shared__ float lds[];
@@ -228,13 +228,14 @@ __global__ __launch_bounds__(GL3_STEP_BLOCK, 1) void decode_step_kernel(ModelDev
     const cLayerDev *L = layers + l;
     SH::QKV::run(ld_mat(&L->qkv), rows_qkv, m.x, L->attn_norm, m.eps, m.qkv, nullptr, blk, nblk, lds, true);
     trace(m, tk++);
+    if (!grid_barrier(gb, ++epoch)) return;
+    trace(m, tk++);
+    // attention streams K/V through the GEMV ring: Wo's tiles are requested after it
+    phase_attention<SH::hd, SH::gqa, SH::BS>(m, l, si.pos, blk, nblk, lds);
+    trace(m, tk++);
     grid_arrive(gb);
     SH::WO::prefetch(ld_mat(&L->wo), SH::dim, blk, nblk);
     if (!grid_wait(gb, ++epoch)) return;
-    trace(m, tk++);
-    phase_attention<SH::LP, SH::gqa, SH::BS>(m, l, si.pos, blk, nblk, lds);
-    trace(m, tk++);
-    if (!grid_barrier(gb, ++epoch)) return;
     trace(m, tk++);
     SH::WO::run(ld_mat(&L->wo), SH::dim, m.att, nullptr, m.eps, m.x, nullptr, blk, nblk, lds, true);
     trace(m, tk++);
@@ -334,13 +335,30 @@ __device__ __forceinline__ unsigned long long splitmix64(unsigned long long z) {
   z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
   return z ^ (z >> 31);
 }
-__global__ void fill_normal_f16_kernel(uint16_t *dst, size_t n, unsigned long long seed) {
+// rows x cols values, row stride `stride`; value (r, c) is draw number r * cols + c of `seed`
+__global__ void fill_normal_f16_kernel(uint16_t *dst, size_t rows, size_t cols, size_t stride,
+                                       unsigned long long seed) {
+  const size_t n = rows * cols;
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
     unsigned long long h = splitmix64(seed ^ splitmix64(i));
     float u1 = ((float)(h >> 40) + 0.5f) * (1.0f / 16777216.0f);
     float u2 = (float)((h >> 16) & 0xFFFFFFull) * (1.0f / 16777216.0f);
     float r = sqrtf(-2.0f * logf(u1));
-    dst[i] = f2h(r * cospif(2.0f * u2));
+    dst[(i / cols) * stride + i % cols] = f2h(r * cospif(2.0f * u2));
+  }
+}
+
+// V cache <-> position-major rows: vt is one kv head's [hd][ctxp] block, rows is
+// [npos][hd] (positions pos0..pos0+npos-1)
+__global__ void vt_copy_kernel(uint16_t *vt, uint16_t *rows, int hd, int ctxp, int pos0, int npos, int to_vt) {
+  const size_t n = (size_t)npos * hd;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    const int t = (int)(i / hd), d = (int)(i % hd);
+    uint16_t *v = vt + (size_t)d * ctxp + pos0 + t;
+    if (to_vt)
+      *v = rows[i];
+    else
+      rows[i] = *v;
   }
 }
 
@@ -365,11 +383,21 @@ hipError_t launch_f16_to_f32(const uint16_t *in, size_t n, float *out, hipStream
   hipLaunchKernelGGL(f16_to_f32_kernel, dim3((unsigned)grid), dim3(256), 0, st, in, n, out);
   return hipGetLastError();
 }
-hipError_t launch_fill_normal_f16(uint16_t *dst, size_t n, unsigned long long seed, hipStream_t st) {
-  size_t grid = (n + 255) / 256;
+hipError_t launch_fill_normal_f16(uint16_t *dst, size_t rows, size_t cols, size_t stride, unsigned long long seed,
+                                  hipStream_t st) {
+  size_t grid = (rows * cols + 255) / 256;
   if (grid > 65536) grid = 65536;
   if (grid == 0) grid = 1;
-  hipLaunchKernelGGL(fill_normal_f16_kernel, dim3((unsigned)grid), dim3(256), 0, st, dst, n, seed);
+  hipLaunchKernelGGL(fill_normal_f16_kernel, dim3((unsigned)grid), dim3(256), 0, st, dst, rows, cols, stride, seed);
+  return hipGetLastError();
+}
+hipError_t launch_vt_copy(uint16_t *vt, uint16_t *rows, int hd, int ctxp, int pos0, int npos, bool to_vt,
+                          hipStream_t st) {
+  size_t grid = ((size_t)npos * hd + 255) / 256;
+  if (grid > 65536) grid = 65536;
+  if (grid == 0) grid = 1;
+  hipLaunchKernelGGL(vt_copy_kernel, dim3((unsigned)grid), dim3(256), 0, st, vt, rows, hd, ctxp, pos0, npos,
+                     to_vt ? 1 : 0);
   return hipGetLastError();
 }
 

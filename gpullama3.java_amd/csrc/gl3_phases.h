@@ -75,6 +75,7 @@ struct DecodeState {
 struct ModelDev {
   int family, fmt, embd_fmt, cls_fmt;  // embd_fmt: FMT_Q8 / FMT_F16 / FMT_F32
   int dim, hidden, n_layers, n_heads, n_kv, hd, q_dim, kv_dim, vocab, ctx;
+  int ctxp;                 // KV cache position stride: ctx rounded up to a multiple of 16
   int max_split;
   float eps, sqrt_hd;
   const LayerDev *layers;
@@ -82,7 +83,8 @@ struct ModelDev {
   Mat cls;                  // classifier [vocab][dim]
   const float *out_norm;
   const float *rope_cos, *rope_sin;  // [ctx][hd/2]
-  uint16_t *kc, *vc;        // fp16 [L][n_kv][ctx][hd]
+  uint16_t *kc;             // fp16 K cache [L][n_kv][ctxp][hd]
+  uint16_t *vc;             // fp16 V cache, transposed: [L][n_kv][hd][ctxp]
   float *x;                 // residual stream [dim]
   float *qkv;               // raw q,k,v [q_dim + 2 kv_dim]
   float *att;               // attention output [q_dim]
@@ -93,12 +95,12 @@ struct ModelDev {
   unsigned long long *best; // argmax keys [2][nbest]
   DecodeState *st;
   int *tokens_out;          // device copy of generated tokens
-  unsigned long long *tstamp;  // optional phase trace: s_memrealtime at each phase boundary (workgroup 0)
+  unsigned long long *tstamp;  // optional phase trace: s_memrealtime at each phase boundary, per workgroup
 };
 
-// Phase trace of the persistent kernel: workgroup 0 stamps the 100 MHz real-time
-// counter when it leaves a phase (before the grid barrier) and when it enters
-// the next one (after the barrier).
+// Phase trace of the persistent kernel: every workgroup stamps the 100 MHz
+// real-time counter when it leaves a phase (before the grid barrier) and when
+// it enters the next one (after the barrier).
 __device__ __forceinline__ void trace(const ModelDev &m, int idx) {
   if (m.tstamp && threadIdx.x == 0) m.tstamp[(size_t)idx * gridDim.x + blockIdx.x] = __builtin_amdgcn_s_memrealtime();
 }
@@ -641,27 +643,35 @@ struct GemvPhase {
 };
 
 // -------------------------------------------------------------- attention
-// Flash-decode over the fp16 KV cache [L][n_kv][ctx][hd].  Work item = (kv
+// Flash-decode over the fp16 KV cache on the matrix cores.  Work item = (kv
 // head, split of positions); the workgroup serves the GQ query heads of the kv
-// head's GQA group, so each K/V row is read from HBM once per group.
+// head's GQA group, so each K/V element is read from HBM once per group.
 //
-// Every wavefront owns positions in steps of PPW = 64/LP: LP lanes hold 8
-// dimensions each of one position's K and V row (16-byte loads), q of all GQ
-// heads in registers, reduce the GQ scores over the LP lanes with DPP and keep
-// an online softmax state (max, sum, o) per lane group in registers.  K/V
-// loads run ATT_DEPTH steps ahead in a register ring.  The lane groups of a
-// wave are merged with shuffles, the waves through LDS, and the splits of a kv
-// head by log-sum-exp in the workgroup that finishes last.
+// The split is cut into tiles of 16 positions; wave w takes tiles w, w+4, ...
+// A tile's K rows ([16][hd], contiguous in the cache) and V columns (the V
+// cache is stored transposed, [hd][ctxp], so 16 positions of one dimension are
+// contiguous) stream into the per-wave LDS ring of the GEMV phases by DMA,
+// DEPTH tiles ahead.  Per tile:
+//   S[16 pos][16 heads] = K[16][hd] . Q^T    v_mfma_f32_16x16x32_f16
+//   online softmax over the tile (scores / sqrt(hd), InferenceCore.java:114-121)
+//   O[16 heads][hd]    += P[16][16] . V     v_mfma_f32_16x16x16_f16
+// q and p are fp32: each is split into fp16 hi + lo parts (hi = fp16(x),
+// lo = fp16(x - hi)) and both products are accumulated, so the scores and
+// outputs carry ~22 significant bits of q and p (K and V are exactly fp16).
+// Heads beyond GQ are zero columns.  The four waves merge through LDS, the
+// splits of a kv head by log-sum-exp in the workgroup that finishes last.
 //
 // q (and, in the split holding `pos`, the new k and v) are read straight into
-// registers together with the RoPE table entries and the first K/V rows, so
-// the preparation costs one memory round trip: the Qwen3 per-head RMSNorm is a
-// lane-group sum, RoPE rotates pairs inside a lane (Llama, interleaved) or
-// across lanes half a head apart (NeoX).  Scores are (q . k) / sqrt(hd)
-// (InferenceCore.java:114-121); norm and RoPE follow InferenceCore.java:82-100,
-// :341-372, :472-491.
+// registers together with their RoPE partners and table entries (one round
+// trip); Qwen3's per-head RMSNorm is a sum over the 4 lanes holding a head
+// (InferenceCore.java:341-347), RoPE follows InferenceCore.java:82-100 / :472-491.
 
-#define ATT_DEPTH 4
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+#define ATT_DEPTH 3
+#define ATT_RING_U4 (4 * 8 * GL3_WAVE)  // ring slot of the GEMV phases (4 waves x 8 KB), in u32x4
 
 __device__ __forceinline__ void rope_pair(float &v0, float &v1, float c, float s) {
   float a = v0 * c - v1 * s;
@@ -670,19 +680,17 @@ __device__ __forceinline__ void rope_pair(float &v0, float &v1, float c, float s
   v1 = b;
 }
 
-// Positions per split: a multiple of the workgroup's positions per step.
+// Positions per split: a multiple of 64 (16-position tiles x 4 waves).
 __host__ __device__ __forceinline__ int att_split_len(int n, int max_split, int step) {
   int s = (n + max_split - 1) / max_split;
   s = (s + step - 1) / step * step;
   return s < step ? step : s;
 }
 
-// LDS floats of the attention phase: lane-group states o [PPB][G][hd], (m, l)
-// [PPB][G][2] and a flag, with PPB = 64 / LP lane groups per wave x wpb waves.
+// LDS floats of the attention phase: per-wave o [wpb][G][hd], (m, l) [wpb][G][2] and a flag.
 __host__ __device__ __forceinline__ int att_lds_floats(int hd, int G, int wpb, int max_split) {
   (void)max_split;
-  const int ppb = (GL3_WAVE / (hd <= 64 ? 8 : 16)) * wpb;
-  return ppb * G * (hd + 2) + 16;
+  return wpb * G * (hd + 2) + 16;
 }
 
 __device__ __forceinline__ void f4_to(float *dst, float4 v) {
@@ -692,270 +700,356 @@ __device__ __forceinline__ void f4_to(float *dst, float4 v) {
   dst[3] = v.w;
 }
 
-// Qwen3 per-head RMSNorm of the 8 dims a lane holds (lane group = one head):
-// v = w * (ss * v), ss = 1/sqrt(mean(v^2) + eps)  (InferenceCore.java:341-347)
-template <int LP>
-__device__ __forceinline__ void head_norm(float (&v)[8], const float (&w)[8], int hd, float eps) {
-  float ss = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) ss += v[i] * v[i];
-  ss = group_sum<LP>(ss);
-  ss /= (float)hd;
-  ss += eps;
-  ss = (float)(1.0 / sqrt((double)ss));
-#pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = w[i] * (ss * v[i]);
+// Rotation of the K tile's 16-byte chunks inside a row, chosen so that the 16
+// rows read by one MFMA operand load fall in distinct LDS bank groups.
+template <int NQ>
+__device__ __forceinline__ int kswz(int pos) {
+  return NQ == 16 ? pos : (NQ == 8 ? (pos >> 1) : (pos >> 2));
 }
 
-// RoPE of the 8 dims d0..d0+7 a lane holds.  Llama: pairs (2i, 2i+1) with
-// table entry i (c, s hold entries d0/2 .. d0/2+3).  NeoX: pairs (i, i+hd/2)
-// with entry i; the partner dims live in lane `partner` (c, s hold entries
-// (d0 mod hd/2) .. +7).  Inactive lanes (d0 >= hd) take part in the shuffle only.
-__device__ __forceinline__ void rope_lane(float (&v)[8], const float (&c)[8], const float (&s)[8], bool neox,
-                                          bool low, int partner) {
+// RoPE table entries of the 8 dims d0..d0+7 (Llama: entries d0/2.., 4 used;
+// NeoX: entries (d0 mod half)..).
+__device__ __forceinline__ void rope_entries(const ModelDev &m, int pos, int d0, int half, bool neox, float (&c)[8],
+                                             float (&sn)[8]) {
+  // all elements are assigned outside the branch, so the arrays stay in registers
+  const int te = neox ? (d0 < half ? d0 : d0 - half) : d0 / 2;
+  const float *cr = m.rope_cos + (size_t)pos * half + te, *ci = m.rope_sin + (size_t)pos * half + te;
+  const float4 c0 = *(const float4 *)cr, s0 = *(const float4 *)ci;
+  float4 c1 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), s1 = c1;
+  if (neox) {
+    c1 = *(const float4 *)(cr + 4);
+    s1 = *(const float4 *)(ci + 4);
+  }
+  f4_to(&c[0], c0);
+  f4_to(&c[4], c1);
+  f4_to(&sn[0], s0);
+  f4_to(&sn[4], s1);
+}
+
+// RoPE of the 8 dims d0.. of a lane: Llama pairs (2i, 2i+1) inside the lane;
+// NeoX pairs (i, i + half) with the partner values `par`.
+__device__ __forceinline__ void rope_apply(float (&v)[8], const float (&par)[8], const float (&c)[8],
+                                           const float (&sn)[8], bool neox, bool low) {
   if (!neox) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) rope_pair(v[2 * i], v[2 * i + 1], c[i], s[i]);
+    for (int i = 0; i < 4; ++i) rope_pair(v[2 * i], v[2 * i + 1], c[i], sn[i]);
   } else {
-    float o[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = __shfl(v[i], partner);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      float v0 = low ? v[i] : o[i], v1 = low ? o[i] : v[i];
-      rope_pair(v0, v1, c[i], s[i]);
+      float v0 = low ? v[i] : par[i], v1 = low ? par[i] : v[i];
+      rope_pair(v0, v1, c[i], sn[i]);
       v[i] = low ? v0 : v1;
     }
   }
 }
 
-template <int LP, int GQ, int BS>
+__device__ __forceinline__ float inv_rms(float ss, int hd, float eps) {
+  ss /= (float)hd;
+  ss += eps;
+  return (float)(1.0 / sqrt((double)ss));
+}
+
+template <int HD, int GQ, int BS>
 __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, int nblk, float *lds) {
-  constexpr int WPB = BS / GL3_WAVE, PPW = GL3_WAVE / LP, PPB = PPW * WPB;
-  const int hd = m.hd, half = hd / 2;
+  constexpr int WPB = BS / GL3_WAVE;
+  constexpr int NQ = HD / 8;           // 16-byte chunks of a K row
+  constexpr int NC = HD / 32;          // 32-dim chunks (score MFMAs per tile and hi/lo)
+  constexpr int NB = HD / 16;          // 16-dim blocks of the output
+  constexpr int NKI = HD / 32;         // DMA loads of a K tile (16 rows x HD x 2 B = NKI KB)
+  constexpr int NVI = HD / 32;         // DMA loads of a V tile
+  constexpr int NI = NKI + NVI;
+  constexpr int KT_U4 = 16 * NQ;       // K tile size in u32x4
+  static_assert(WPB == 4 && HD % 32 == 0 && HD <= 128 && GQ <= 8, "attention tile shape");
+  const int hd = HD, half = HD / 2;
   const int n = pos + 1;
-  const int S = att_split_len(n, m.max_split, PPB);
+  const int S = att_split_len(n, m.max_split, 16 * WPB);
   const int nsplit = (n + S - 1) / S;
   const int items = m.n_kv * nsplit;
   const int hpart = hd + 4;
-  static_assert(LP == 8 || LP == 16, "lane group");
-  float *opart = lds;                     // lane-group o [PPB][GQ][hd]
-  float *mlp = opart + PPB * GQ * hd;     // lane-group (m, l) [PPB][GQ][2]
-  int *flag = (int *)(mlp + PPB * GQ * 2);
+  float *opart = lds;                     // per-wave o [WPB][GQ][hd]
+  float *mlp = opart + WPB * GQ * hd;     // per-wave (m, l) [WPB][GQ][2]
+  int *flag = (int *)(mlp + WPB * GQ * 2);
   const LayerDev L = ld_layer(m.layers, layer);
-  const size_t head_stride = (size_t)m.ctx * hd;
-  uint16_t *kc_l = m.kc + (size_t)layer * m.n_kv * head_stride;
-  uint16_t *vc_l = m.vc + (size_t)layer * m.n_kv * head_stride;
   const int wave = wave_id(), lane = lane_id();
-  const int grp = lane / LP, sub = lane % LP, d0 = 8 * sub;
-  const bool act = d0 < hd;
-  const bool neox = m.family != FAM_LLAMA;
-  const bool low = d0 < half;
-  const int partner = (lane - sub) + (low ? sub + half / 8 : sub - half / 8);
-  const bool qwen = m.family == FAM_QWEN3;
-  const int te = neox ? (low ? d0 : d0 - half) : d0 / 2;  // first RoPE table entry of the lane
+  const int hh = lane % 16, kb = lane / 16;  // MFMA column (head) and k-block of this lane
+  const bool neox = m.family != FAM_LLAMA, qwen = m.family == FAM_QWEN3;
+  u32x4 *ring0 = ring_w<0, ATT_RING_U4>() + wave * 8 * GL3_WAVE;
+  u32x4 *ring1 = ring_w<1, ATT_RING_U4>() + wave * 8 * GL3_WAVE;
+  u32x4 *ring2 = ring_w<2, ATT_RING_U4>() + wave * 8 * GL3_WAVE;
 
   for (int item = blk; item < items; item += nblk) {
     const int kvh = item / nsplit, sp = item % nsplit;
     const int t0 = sp * S, t1 = min(n, t0 + S);
     const bool owns_pos = (pos >= t0 && pos < t1);
-    uint16_t *kh = kc_l + kvh * head_stride;
-    uint16_t *vh = vc_l + kvh * head_stride;
-    const int tb0 = t0 + wave * PPW + grp;
+    const int ntile = (t1 - t0 + 15) / 16;
+    const int ntw = wave < ntile ? (ntile - 1 - wave) / WPB + 1 : 0;  // tiles of this wave
+    uint16_t *kbase = m.kc + ((size_t)layer * m.n_kv + kvh) * m.ctxp * HD;
+    uint16_t *vbase = m.vc + ((size_t)layer * m.n_kv + kvh) * HD * m.ctxp;
+    const __amdgpu_buffer_rsrc_t rk = rsrc(kbase), rv = rsrc(vbase);
 
-    // ---- one round trip: q, new k/v, RoPE entries, norm weights, first K/V rows
-    float qr[GQ][8], kn[8], vn[8], rc[8], rs[8], qw[8], kw8[8];
-    if (act) {
+    // DMA of this wave's u-th tile into ring slot `slot`
+    auto issue = [&](u32x4 *slot, int u) __attribute__((always_inline)) {
+      const int t = t0 + 16 * (wave + WPB * u);
+      wait_lds();
 #pragma unroll
-      for (int g = 0; g < GQ; ++g) {
-        const unsigned qo = (unsigned)((kvh * GQ + g) * hd + d0);
-        f4_to(&qr[g][0], ld_coherent_f4(m.qkv, qo));
-        f4_to(&qr[g][4], ld_coherent_f4(m.qkv, qo + 4));
+      for (int i = 0; i < NKI; ++i) {
+        const int ci = GL3_WAVE * i + lane, p = ci / NQ;
+        int q = ci % NQ - kswz<NQ>(p);
+        q = q < 0 ? q + NQ : q;
+        dma16(rk, slot + GL3_WAVE * i, (unsigned)(((t + p) * HD + 8 * q) * 2), 0u);
       }
-      if (owns_pos) {
-        const unsigned ko = (unsigned)(m.q_dim + kvh * hd + d0), vo = ko + (unsigned)m.kv_dim;
-        f4_to(&kn[0], ld_coherent_f4(m.qkv, ko));
-        f4_to(&kn[4], ld_coherent_f4(m.qkv, ko + 4));
-        f4_to(&vn[0], ld_coherent_f4(m.qkv, vo));
-        f4_to(&vn[4], ld_coherent_f4(m.qkv, vo + 4));
+#pragma unroll
+      for (int i = 0; i < NVI; ++i) {
+        const int d = 32 * i + lane / 2;
+        dma16(rv, slot + KT_U4 + GL3_WAVE * i, (unsigned)((d * m.ctxp + t + 8 * (lane % 2)) * 2), 0u);
       }
-      const float *cr = m.rope_cos + (size_t)pos * half + te, *ci = m.rope_sin + (size_t)pos * half + te;
-      f4_to(&rc[0], *(const float4 *)cr);
-      f4_to(&rs[0], *(const float4 *)ci);
-      if (neox) {
-        f4_to(&rc[4], *(const float4 *)(cr + 4));
-        f4_to(&rs[4], *(const float4 *)(ci + 4));
+    };
+    if (ntw > 0) issue(ring0, 0);
+    if (ntw > 1) issue(ring1, 1);
+    if (ntw > 2) issue(ring2, 2);
+
+    // ---- q of head hh (columns >= GQ stay zero), the new k and v: one round trip
+    float qv[NC][8];
+    {
+      float wv[NC][8], cs[NC][8], sn[NC][8];
+      float ss = 0.0f;
+      // lanes of columns >= GQ load head 0 and keep zeros (no divergent writes:
+      // the arrays stay in registers)
+      const bool qok = hh < GQ;
+      const float *src = m.qkv + (size_t)(kvh * GQ + (qok ? hh : 0)) * hd;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int d0 = 32 * c + 8 * kb;
+        const float4 a0 = ld_coherent_f4(src, (unsigned)d0), a1 = ld_coherent_f4(src, (unsigned)d0 + 4);
+        float4 w0 = make_float4(1.0f, 1.0f, 1.0f, 1.0f), w1 = w0;
+        if (qwen) {
+          w0 = *(const float4 *)(L.q_norm + d0);
+          w1 = *(const float4 *)(L.q_norm + d0 + 4);
+        }
+        f4_to(&qv[c][0], a0);
+        f4_to(&qv[c][4], a1);
+        f4_to(&wv[c][0], w0);
+        f4_to(&wv[c][4], w1);
+        rope_entries(m, pos, d0, half, neox, cs[c], sn[c]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          qv[c][i] = qok ? qv[c][i] : 0.0f;
+          ss += qv[c][i] * qv[c][i];
+        }
       }
       if (qwen) {
-        f4_to(&qw[0], *(const float4 *)(L.q_norm + d0));
-        f4_to(&qw[4], *(const float4 *)(L.q_norm + d0 + 4));
-        f4_to(&kw8[0], *(const float4 *)(L.k_norm + d0));
-        f4_to(&kw8[4], *(const float4 *)(L.k_norm + d0 + 4));
+        ss += __shfl_xor(ss, 16);
+        ss += __shfl_xor(ss, 32);
+        const float si = inv_rms(ss, hd, m.eps);
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) qv[c][i] = wv[c][i] * (si * qv[c][i]);
       }
-    } else {
+      if (neox) {
+        // partner dims (d +- hd/2) are exchanged through this wave's part of the
+        // partial buffer (unused until the end of the item); one wave, so the
+        // reads see the writes
+        float *xs = opart + wave * GQ * hd + (qok ? hh : 0) * hd;
+        if (qok) {
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            const int d0 = 32 * c + 8 * kb;
+            *(float4 *)(xs + d0) = make_float4(qv[c][0], qv[c][1], qv[c][2], qv[c][3]);
+            *(float4 *)(xs + d0 + 4) = make_float4(qv[c][4], qv[c][5], qv[c][6], qv[c][7]);
+          }
+        }
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const int d0 = 32 * c + 8 * kb, pd = d0 < half ? d0 + half : d0 - half;
+          float par[8];
+          f4_to(&par[0], *(const float4 *)(xs + pd));
+          f4_to(&par[4], *(const float4 *)(xs + pd + 4));
+          rope_apply(qv[c], par, cs[c], sn[c], true, d0 < half);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) qv[c][i] = qok ? qv[c][i] : 0.0f;
+        }
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+      } else {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) rope_apply(qv[c], qv[c], cs[c], sn[c], false, true);
+      }
+    }
+    half8 qh[NC], ql[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-#pragma unroll
-        for (int g = 0; g < GQ; ++g) qr[g][i] = 0.0f;
-        kn[i] = vn[i] = rc[i] = rs[i] = qw[i] = kw8[i] = 0.0f;
+        const _Float16 h16 = (_Float16)qv[c][i];
+        qh[c][i] = h16;
+        ql[c][i] = (_Float16)(qv[c][i] - (float)h16);
       }
-    }
-    u32x4 kr[ATT_DEPTH], vr[ATT_DEPTH];
+    // new k, v (fp16 bits) of the 8 dims 8*lane.. held by lanes < NQ
+    unsigned knb[4] = {0u, 0u, 0u, 0u}, vnb[4] = {0u, 0u, 0u, 0u};
+    const int wpos = owns_pos ? ((pos - t0) / 16) % WPB : -1;  // wave whose tile holds pos
+    if (wave == wpos) {
+      float kv[8], vv[8], kw[8], cs[8], sn[8], par[8];
+      float ss = 0.0f;
+      const bool kok = lane < NQ;
+      const int d0 = 8 * (kok ? lane : 0);
+      {
+        const unsigned ko = (unsigned)(m.q_dim + kvh * hd + d0), vo = ko + (unsigned)m.kv_dim;
+        f4_to(&kv[0], ld_coherent_f4(m.qkv, ko));
+        f4_to(&kv[4], ld_coherent_f4(m.qkv, ko + 4));
+        f4_to(&vv[0], ld_coherent_f4(m.qkv, vo));
+        f4_to(&vv[4], ld_coherent_f4(m.qkv, vo + 4));
+        float4 w0 = make_float4(1.0f, 1.0f, 1.0f, 1.0f), w1 = w0;
+        if (qwen) {
+          w0 = *(const float4 *)(L.k_norm + d0);
+          w1 = *(const float4 *)(L.k_norm + d0 + 4);
+        }
+        f4_to(&kw[0], w0);
+        f4_to(&kw[4], w1);
+        rope_entries(m, pos, d0, half, neox, cs, sn);
 #pragma unroll
-    for (int u = 0; u < ATT_DEPTH; ++u) {
-      const int t = tb0 + u * PPB;
-      if (act && t < t1 && t != pos) {
-        kr[u] = ld_stream(kh + (size_t)t * hd + d0);
-        vr[u] = ld_stream(vh + (size_t)t * hd + d0);
-      } else {
-        kr[u] = u32x4{0u, 0u, 0u, 0u};
-        vr[u] = u32x4{0u, 0u, 0u, 0u};
+        for (int i = 0; i < 8; ++i) ss += kok ? kv[i] * kv[i] : 0.0f;
       }
-    }
-    // ---- q (and new k): per-head norm (Qwen3), RoPE at pos
+      if (qwen) {
+        const float si = inv_rms(row16_sum(ss), hd, m.eps);
 #pragma unroll
-    for (int g = 0; g < GQ; ++g) {
-      if (qwen) head_norm<LP>(qr[g], qw, hd, m.eps);
-      rope_lane(qr[g], rc, rs, neox, low, partner);
-    }
-    if (owns_pos) {
-      if (qwen) head_norm<LP>(kn, kw8, hd, m.eps);
-      rope_lane(kn, rc, rs, neox, low, partner);
-      // fp16 cache entries at pos; the values used below are the rounded ones
-      unsigned kb[4], vb[4];
+        for (int i = 0; i < 8; ++i) kv[i] = kw[i] * (si * kv[i]);
+      }
+      // NeoX partner dims d +- hd/2 live in lane +- hd/16
+      const int pl = d0 < half ? lane + half / 8 : lane - half / 8;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) par[i] = __shfl(kv[i], pl < 0 ? 0 : pl);
+      rope_apply(kv, par, cs, sn, neox, d0 < half);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint16_t k0 = f2h(kn[2 * i]), k1 = f2h(kn[2 * i + 1]);
-        const uint16_t v0 = f2h(vn[2 * i]), v1 = f2h(vn[2 * i + 1]);
-        kb[i] = (unsigned)k0 | ((unsigned)k1 << 16);
-        vb[i] = (unsigned)v0 | ((unsigned)v1 << 16);
-        kn[2 * i] = h2f(k0);
-        kn[2 * i + 1] = h2f(k1);
-        vn[2 * i] = h2f(v0);
-        vn[2 * i + 1] = h2f(v1);
+        knb[i] = (unsigned)f2h(kv[2 * i]) | ((unsigned)f2h(kv[2 * i + 1]) << 16);
+        vnb[i] = (unsigned)f2h(vv[2 * i]) | ((unsigned)f2h(vv[2 * i + 1]) << 16);
       }
-      if (wave == 0 && grp == 0 && act) {
-        *(u32x4 *)(kh + (size_t)pos * hd + d0) = u32x4{kb[0], kb[1], kb[2], kb[3]};
-        *(u32x4 *)(vh + (size_t)pos * hd + d0) = u32x4{vb[0], vb[1], vb[2], vb[3]};
+      if (kok) {
+        // append to the cache (read by later steps)
+        *(u32x4 *)(kbase + (size_t)pos * HD + d0) = u32x4{knb[0], knb[1], knb[2], knb[3]};
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          vbase[(size_t)(d0 + i) * m.ctxp + pos] = (uint16_t)(vnb[i / 2] >> (16 * (i % 2)));
       }
     }
 
-    float mr[GQ], lr[GQ], o[GQ][8];
+    // ---- tiles
+    f32x4 O[NB];
 #pragma unroll
-    for (int g = 0; g < GQ; ++g) {
-      mr[g] = -INFINITY;
-      lr[g] = 0.0f;
+    for (int b = 0; b < NB; ++b) O[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float mrun = -INFINITY, lrun = 0.0f;
+    auto tile = [&](u32x4 *slot, int u) __attribute__((always_inline)) {
+      const int t = t0 + 16 * (wave + WPB * u);
+      const int nvalid = min(16, t1 - t);
+      // the new position and the tail of a partial tile are written into the LDS tile
+      if (pos >= t && pos < t + 16) {
+        const int pl = pos - t;
+        if (lane < NQ) {
+          slot[pl * NQ + (lane + kswz<NQ>(pl)) % NQ] = u32x4{knb[0], knb[1], knb[2], knb[3]};
+          uint16_t *vt = (uint16_t *)(slot + KT_U4);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) o[g][i] = 0.0f;
+          for (int i = 0; i < 8; ++i) vt[(8 * lane + i) * 16 + pl] = (uint16_t)(vnb[i / 2] >> (16 * (i % 2)));
+        }
+      }
+      if (nvalid < 16) {
+        uint16_t *vt = (uint16_t *)(slot + KT_U4);
+        for (int idx = lane; idx < HD * 16; idx += GL3_WAVE)
+          if (idx % 16 >= nvalid) vt[idx] = 0;
+      }
+      // scores
+      f32x4 sacc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int p = hh, q = 4 * c + kb;
+        const u32x4 w = slot[p * NQ + (q + kswz<NQ>(p)) % NQ];
+        const half8 a = __builtin_bit_cast(half8, w);
+        sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[c], sacc, 0, 0, 0);
+        sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[c], sacc, 0, 0, 0);
+      }
+      // lane: head hh, positions 4*kb + v
+      float sv[4];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const bool ok = hh < GQ && 4 * kb + v < nvalid;
+        sv[v] = ok ? sacc[v] / m.sqrt_hd : -INFINITY;
+        mx = fmaxf(mx, sv[v]);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float mn = fmaxf(mrun, mx);
+      const float cf = (mrun == -INFINITY) ? 0.0f : __expf(mrun - mn);
+      float p4[4], ls = 0.0f;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        p4[v] = (sv[v] == -INFINITY) ? 0.0f : __expf(sv[v] - mn);
+        ls += p4[v];
+      }
+      ls += __shfl_xor(ls, 16);
+      ls += __shfl_xor(ls, 32);
+      if (mn != -INFINITY) {
+        lrun = lrun * cf + ls;
+        mrun = mn;
+      }
+      // O rows are heads 4*kb + v: their rescale factors live in lanes 4*kb + v
+      float cr[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float cv = __shfl(cf, 4 * kb + v);
+        const float mv = __shfl(mn, 4 * kb + v);
+        cr[v] = (mv == -INFINITY) ? 1.0f : cv;
+      }
+      half4 ph, pl;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const _Float16 h16 = (_Float16)p4[v];
+        ph[v] = h16;
+        pl[v] = (_Float16)(p4[v] - (float)h16);
+      }
+      const uint2 *vt2 = (const uint2 *)(slot + KT_U4);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) O[b][v] *= cr[v];
+        const uint2 w = vt2[(16 * b + hh) * 4 + kb];  // V^T row 16b+hh, positions 4kb..4kb+3
+        const half4 vb = __builtin_bit_cast(half4, w);
+        O[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, vb, O[b], 0, 0, 0);
+        O[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, vb, O[b], 0, 0, 0);
+      }
+    };
+    for (int u = 0; u < ntw; u += ATT_DEPTH) {
+      // slot s is complete once at most the loads of the later issued tiles are outstanding
+#define GL3_ATT_STEP(SLOT, K)                                                       \
+      if (u + K < ntw) {                                                            \
+        const int later = ntw - 1 - (u + K);                                        \
+        if (later >= 2) wait_vmem<2 * NI>();                                        \
+        else if (later == 1) wait_vmem<NI>();                                       \
+        else wait_vmem<0>();                                                        \
+        tile(SLOT, u + K);                                                          \
+        if (u + K + ATT_DEPTH < ntw) issue(SLOT, u + K + ATT_DEPTH);                \
+      }
+      GL3_ATT_STEP(ring0, 0)
+      GL3_ATT_STEP(ring1, 1)
+      GL3_ATT_STEP(ring2, 2)
+#undef GL3_ATT_STEP
     }
-    // ---- scores and softmax, ATT_DEPTH steps per batch: all scores of the
-    //      batch first, one rescale of the running state, then the V terms.
-    //      Slot u of the register ring is reloaded ATT_DEPTH steps ahead right
-    //      after use; steps past the split's end are skipped by the wave.
-    const int wb = __builtin_amdgcn_readfirstlane(t0 + wave * PPW);  // the wave's first position
-    for (int it = 0; wb + it * ATT_DEPTH * PPB < t1; ++it) {
-      const int tb = tb0 + it * ATT_DEPTH * PPB, wt = wb + it * ATT_DEPTH * PPB;
-      float sc[ATT_DEPTH][GQ], bm[GQ];
+    // ---- wave partials to LDS: O rows (heads) 4*kb + v, columns (dims) 16b + hh
 #pragma unroll
-      for (int g = 0; g < GQ; ++g) bm[g] = -INFINITY;
+    for (int b = 0; b < NB; ++b)
 #pragma unroll
-      for (int u = 0; u < ATT_DEPTH; ++u) {
-#pragma unroll
-        for (int g = 0; g < GQ; ++g) sc[u][g] = -INFINITY;
-        if (wt + u * PPB < t1) {
-          const int t = tb + u * PPB;
-          float kf[8];
-          if (t == pos) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) kf[i] = kn[i];
-          } else {
-            const unsigned ka[4] = {kr[u].x, kr[u].y, kr[u].z, kr[u].w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              kf[2 * i] = h2f_lo(ka[i]);
-              kf[2 * i + 1] = h2f_hi(ka[i]);
-            }
-          }
-          const int tn = t + ATT_DEPTH * PPB;
-          if (act && tn < t1 && tn != pos) kr[u] = ld_stream(kh + (size_t)tn * hd + d0);
-#pragma unroll
-          for (int g = 0; g < GQ; ++g) {
-            float a = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) a = fmaf(qr[g][i], kf[i], a);
-            const float sv = group_sum<LP>(a) / m.sqrt_hd;
-            if (t < t1) {
-              sc[u][g] = sv;
-              bm[g] = fmaxf(bm[g], sv);
-            }
-          }
-        }
+      for (int v = 0; v < 4; ++v) {
+        const int g = 4 * kb + v;
+        if (g < GQ) opart[(wave * GQ + g) * hd + 16 * b + hh] = O[b][v];
       }
-#pragma unroll
-      for (int g = 0; g < GQ; ++g) {
-        const float mn = fmaxf(mr[g], bm[g]);
-        if (mn != -INFINITY) {
-          const float c = __expf(mr[g] - mn);
-          lr[g] *= c;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) o[g][i] *= c;
-          mr[g] = mn;
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < ATT_DEPTH; ++u) {
-        if (wt + u * PPB < t1) {
-          const int t = tb + u * PPB;
-          float vf[8];
-          if (t == pos) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) vf[i] = vn[i];
-          } else {
-            const unsigned va[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              vf[2 * i] = h2f_lo(va[i]);
-              vf[2 * i + 1] = h2f_hi(va[i]);
-            }
-          }
-          const int tn = t + ATT_DEPTH * PPB;
-          if (act && tn < t1 && tn != pos) vr[u] = ld_stream(vh + (size_t)tn * hd + d0);
-#pragma unroll
-          for (int g = 0; g < GQ; ++g) {
-            if (sc[u][g] != -INFINITY) {
-              const float p = __expf(sc[u][g] - mr[g]);
-              lr[g] += p;
-#pragma unroll
-              for (int i = 0; i < 8; ++i) o[g][i] = fmaf(p, vf[i], o[g][i]);
-            }
-          }
-        }
-      }
-    }
-    // ---- the PPB lane-group states of the workgroup go to LDS; thread (g, d)
-    //      pairs merge them
-    {
-      const int pi = wave * PPW + grp;
-      if (act) {
-#pragma unroll
-        for (int g = 0; g < GQ; ++g) {
-          float *dst = opart + (pi * GQ + g) * hd + d0;
-          *(float4 *)dst = make_float4(o[g][0], o[g][1], o[g][2], o[g][3]);
-          *(float4 *)(dst + 4) = make_float4(o[g][4], o[g][5], o[g][6], o[g][7]);
-        }
-      }
-      if (sub == 0) {
-#pragma unroll
-        for (int g = 0; g < GQ; ++g) {
-          mlp[(pi * GQ + g) * 2] = mr[g];
-          mlp[(pi * GQ + g) * 2 + 1] = lr[g];
-        }
-      }
+    if (kb == 0 && hh < GQ) {
+      mlp[(wave * GQ + hh) * 2] = mrun;
+      mlp[(wave * GQ + hh) * 2 + 1] = lrun;
     }
     __syncthreads();
-    constexpr int PAIRS = (GQ * LP * 8 + BS - 1) / BS;  // per-thread (g, d) slots (hd <= 8 * LP)
-    constexpr int CB = 8;                                 // partials read per batch
-    static_assert(PPB % CB == 0, "lane-group partials per batch");
+    constexpr int PAIRS = (GQ * HD + BS - 1) / BS;  // per-thread (g, d) slots
     float Ofin[PAIRS], Mfin[PAIRS], Lfin[PAIRS];
 #pragma unroll
     for (int k = 0; k < PAIRS; ++k) {
@@ -965,35 +1059,26 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
       const int idx = threadIdx.x + k * BS;
       if (idx < GQ * hd) {
         const int g = idx / hd, d = idx % hd;
-        // LDS reads are issued CB at a time before their first use (one wave per
-        // SIMD: nothing else hides their latency)
-        float M = -INFINITY;
-        for (int p0 = 0; p0 < PPB; p0 += CB) {
-          float mv[CB];
+        float mv[WPB], lv[WPB], ov[WPB];
 #pragma unroll
-          for (int c = 0; c < CB; ++c) mv[c] = mlp[((p0 + c) * GQ + g) * 2];
-#pragma unroll
-          for (int c = 0; c < CB; ++c) M = fmaxf(M, mv[c]);
+        for (int w = 0; w < WPB; ++w) {
+          mv[w] = mlp[(w * GQ + g) * 2];
+          lv[w] = mlp[(w * GQ + g) * 2 + 1];
+          ov[w] = opart[(w * GQ + g) * hd + d];
         }
-        float Ls = 0.0f, O = 0.0f;
-        for (int p0 = 0; p0 < PPB; p0 += CB) {
-          float mv[CB], lv[CB], ov[CB];
+        float M = -INFINITY;
 #pragma unroll
-          for (int c = 0; c < CB; ++c) {
-            mv[c] = mlp[((p0 + c) * GQ + g) * 2];
-            lv[c] = mlp[((p0 + c) * GQ + g) * 2 + 1];
-            ov[c] = opart[((p0 + c) * GQ + g) * hd + d];
-          }
+        for (int w = 0; w < WPB; ++w) M = fmaxf(M, mv[w]);
+        float Ls = 0.0f, Ov = 0.0f;
 #pragma unroll
-          for (int c = 0; c < CB; ++c) {
-            const float w = (mv[c] == -INFINITY) ? 0.0f : __expf(mv[c] - M);
-            Ls = fmaf(lv[c], w, Ls);
-            O = fmaf(ov[c], w, O);
-          }
+        for (int w = 0; w < WPB; ++w) {
+          const float wt = (mv[w] == -INFINITY) ? 0.0f : __expf(mv[w] - M);
+          Ls = fmaf(lv[w], wt, Ls);
+          Ov = fmaf(ov[w], wt, Ov);
         }
         Mfin[k] = M;
         Lfin[k] = Ls;
-        Ofin[k] = O;
+        Ofin[k] = Ov;
       }
     }
     if (nsplit == 1) {

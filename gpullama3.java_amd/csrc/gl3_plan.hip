@@ -296,6 +296,7 @@ extern "C" int gl3_create(const gl3_config *cfg, gl3_plan **out) {
   m.kv_dim = p->kv_dim;
   m.vocab = cfg->vocab_size;
   m.ctx = cfg->context_length;
+  m.ctxp = (cfg->context_length + 15) / 16 * 16;
   m.eps = cfg->rms_norm_eps;
   m.sqrt_hd = (float)std::sqrt((double)hd);  // (float) Math.sqrt(headSize), InferenceCore.java:64
   // about one attention work item (kv head, split) per CU
@@ -303,7 +304,7 @@ extern "C" int gl3_create(const gl3_config *cfg, gl3_plan **out) {
   m.max_split = ms < 1 ? 1 : (ms > 256 ? 256 : ms);
   m.out_norm = p->out_norm;
   m.layers = p->layers_d;
-  size_t kv_elems = (size_t)L * cfg->n_kv_heads * cfg->context_length * hd;
+  size_t kv_elems = (size_t)L * cfg->n_kv_heads * m.ctxp * hd;
   TRY(dev_alloc(p, &m.kc, kv_elems));
   TRY(dev_alloc(p, &m.vc, kv_elems));
   float *rc_ = nullptr, *rs_ = nullptr;
@@ -741,35 +742,45 @@ extern "C" int gl3_generate_greedy(gl3_plan *p, int32_t token, int32_t position,
 
 extern "C" int gl3_reset(gl3_plan *p) {
   if (!p) return fail(GL3_ERR_INVALID_ARGUMENT, "null plan");
-  size_t kv = (size_t)p->cfg.n_layers * p->cfg.n_kv_heads * p->cfg.context_length * p->cfg.head_dim * 2;
+  size_t kv = (size_t)p->cfg.n_layers * p->cfg.n_kv_heads * p->m.ctxp * p->cfg.head_dim * 2;
   HIP_TRY(hipMemsetAsync(p->m.kc, 0, kv, p->stream));
   HIP_TRY(hipMemsetAsync(p->m.vc, 0, kv, p->stream));
   HIP_TRY(hipStreamSynchronize(p->stream));
   return GL3_OK;
 }
 
-// KV cache: device [L][n_kv][ctx][hd], host [npos][n_kv*hd]
+// KV cache: device K [L][n_kv][ctxp][hd] and V [L][n_kv][hd][ctxp]; host [npos][n_kv*hd]
 static int kv_copy(gl3_plan *p, int layer, int pos0, int npos, uint16_t *host_k, uint16_t *host_v, bool to_device) {
   const gl3_config &c = p->cfg;
   if (layer < 0 || layer >= c.n_layers || pos0 < 0 || npos < 0 || (int64_t)pos0 + npos > c.context_length)
     return fail(GL3_ERR_INVALID_ARGUMENT, "kv range layer %d [%d,%d) outside the cache", layer, pos0, pos0 + npos);
   if (!host_k || !host_v) return fail(GL3_ERR_INVALID_ARGUMENT, "null buffer");
-  const int hd = c.head_dim, nkv = c.n_kv_heads;
-  for (int h = 0; h < nkv; ++h) {
-    size_t dev_off = (((size_t)layer * nkv + h) * c.context_length + pos0) * hd;
-    // one strided 2-D copy per head: device rows of hd, host rows of kv_dim
-    hipMemcpyKind kind = to_device ? hipMemcpyHostToDevice : hipMemcpyDeviceToHost;
-    for (int which = 0; which < 2; ++which) {
-      uint16_t *dev = (which ? p->m.vc : p->m.kc) + dev_off;
-      uint16_t *host = (which ? host_v : host_k) + (size_t)h * hd;
-      if (to_device)
-        HIP_TRY(hipMemcpy2DAsync(dev, hd * 2, host, (size_t)p->kv_dim * 2, hd * 2, npos, kind, p->stream));
-      else
-        HIP_TRY(hipMemcpy2DAsync(host, (size_t)p->kv_dim * 2, dev, hd * 2, hd * 2, npos, kind, p->stream));
+  if (npos == 0) return GL3_OK;
+  const int hd = c.head_dim, nkv = c.n_kv_heads, ctxp = p->m.ctxp;
+  const hipMemcpyKind kind = to_device ? hipMemcpyHostToDevice : hipMemcpyDeviceToHost;
+  uint16_t *stage = nullptr;  // one head's V rows [npos][hd]
+  hipError_t he = hipMallocAsync((void **)&stage, (size_t)npos * hd * 2, p->stream);
+  if (he != hipSuccess) return fail(GL3_ERR_OUT_OF_MEMORY, "kv staging: %s", hipGetErrorString(he));
+  int rc = GL3_OK;
+  for (int h = 0; h < nkv && rc == GL3_OK; ++h) {
+    uint16_t *kdev = p->m.kc + (((size_t)layer * nkv + h) * ctxp + pos0) * hd;
+    uint16_t *vt = p->m.vc + ((size_t)layer * nkv + h) * hd * ctxp;
+    uint16_t *hk = host_k + (size_t)h * hd, *hv = host_v + (size_t)h * hd;
+    if (to_device) {
+      he = hipMemcpy2DAsync(kdev, hd * 2, hk, (size_t)p->kv_dim * 2, hd * 2, npos, kind, p->stream);
+      if (he == hipSuccess) he = hipMemcpy2DAsync(stage, hd * 2, hv, (size_t)p->kv_dim * 2, hd * 2, npos, kind, p->stream);
+      if (he == hipSuccess) he = launch_vt_copy(vt, stage, hd, ctxp, pos0, npos, true, p->stream);
+    } else {
+      he = hipMemcpy2DAsync(hk, (size_t)p->kv_dim * 2, kdev, hd * 2, hd * 2, npos, kind, p->stream);
+      if (he == hipSuccess) he = launch_vt_copy(vt, stage, hd, ctxp, pos0, npos, false, p->stream);
+      if (he == hipSuccess) he = hipMemcpy2DAsync(hv, (size_t)p->kv_dim * 2, stage, hd * 2, hd * 2, npos, kind, p->stream);
     }
+    if (he == hipSuccess) he = hipStreamSynchronize(p->stream);  // the staging buffer is reused per head
+    if (he != hipSuccess) rc = fail(GL3_ERR_DEVICE, "kv copy: %s", hipGetErrorString(he));
   }
-  HIP_TRY(hipStreamSynchronize(p->stream));
-  return GL3_OK;
+  hipFreeAsync(stage, p->stream);
+  hipStreamSynchronize(p->stream);
+  return rc;
 }
 
 extern "C" int gl3_write_kv(gl3_plan *p, int layer, int pos0, int npos, const uint16_t *k, const uint16_t *v) {
@@ -785,13 +796,15 @@ extern "C" int gl3_fill_kv_normal(gl3_plan *p, uint64_t seed, int npos) {
   if (!p) return fail(GL3_ERR_INVALID_ARGUMENT, "null plan");
   const gl3_config &c = p->cfg;
   if (npos < 0 || npos > c.context_length) return fail(GL3_ERR_INVALID_ARGUMENT, "npos %d", npos);
-  const size_t per = (size_t)npos * c.head_dim;
+  if (npos == 0) return GL3_OK;
+  const size_t hd = c.head_dim, ctxp = p->m.ctxp;
   for (int l = 0; l < c.n_layers; ++l)
     for (int h = 0; h < c.n_kv_heads; ++h) {
-      size_t off = (((size_t)l * c.n_kv_heads + h) * c.context_length) * c.head_dim;
-      unsigned long long sk = seed ^ (0x100000001B3ull * (unsigned long long)(2 * (l * c.n_kv_heads + h) + 1));
-      HIP_TRY(launch_fill_normal_f16(p->m.kc + off, per, sk, p->stream));
-      HIP_TRY(launch_fill_normal_f16(p->m.vc + off, per, sk ^ 0xA5A5A5A5A5A5A5A5ull, p->stream));
+      const size_t head = (size_t)l * c.n_kv_heads + h;
+      unsigned long long sk = seed ^ (0x100000001B3ull * (unsigned long long)(2 * head + 1));
+      HIP_TRY(launch_fill_normal_f16(p->m.kc + head * ctxp * hd, 1, (size_t)npos * hd, 0, sk, p->stream));
+      HIP_TRY(launch_fill_normal_f16(p->m.vc + head * hd * ctxp, hd, (size_t)npos, ctxp, sk ^ 0xA5A5A5A5A5A5A5A5ull,
+                                     p->stream));
     }
   HIP_TRY(hipStreamSynchronize(p->stream));
   return GL3_OK;
@@ -942,13 +955,16 @@ extern "C" int gl3_op_attention(const float *q, const uint16_t *kcache, const ui
   m.q_dim = q_dim;
   m.kv_dim = kv_dim;
   m.ctx = ctx;
+  m.ctxp = (ctx + 15) / 16 * 16;
   m.sqrt_hd = (float)std::sqrt((double)hd);
   int ms = n_cu / n_kv_heads;
   m.max_split = ms < 1 ? 1 : (ms > 256 ? 256 : ms);
   DevBuf layers, kc, vc, rc_, rs_, qkv, att, part, ctr, st;
   DEV_ALLOC(layers, sizeof(LayerDev));
-  DEV_ALLOC(kc, (size_t)n_kv_heads * ctx * hd * 2);
-  DEV_ALLOC(vc, (size_t)n_kv_heads * ctx * hd * 2);
+  DEV_ALLOC(kc, (size_t)n_kv_heads * m.ctxp * hd * 2);
+  DEV_ALLOC(vc, (size_t)n_kv_heads * m.ctxp * hd * 2);
+  DevBuf vstage;
+  DEV_ALLOC(vstage, (size_t)ctx * hd * 2);
   DEV_ALLOC(rc_, (size_t)ctx * (hd / 2) * 4);
   DEV_ALLOC(rs_, (size_t)ctx * (hd / 2) * 4);
   DEV_ALLOC(qkv, (size_t)(q_dim + 2 * kv_dim) * 4);
@@ -958,12 +974,15 @@ extern "C" int gl3_op_attention(const float *q, const uint16_t *kcache, const ui
   DEV_ALLOC(st, sizeof(DecodeState));
   LayerDev L{};
   HIP_TRY(hipMemcpy(layers.ptr, &L, sizeof L, hipMemcpyHostToDevice));
-  // cache [pos+1][n_kv][hd] (host) -> [n_kv][ctx][hd] (device)
+  // cache [pos+1][n_kv][hd] (host) -> K [n_kv][ctxp][hd], V [n_kv][hd][ctxp] (device)
   for (int h = 0; h < n_kv_heads; ++h) {
-    HIP_TRY(hipMemcpy2D((uint16_t *)kc.ptr + (size_t)h * ctx * hd, hd * 2, kcache + (size_t)h * hd, (size_t)kv_dim * 2,
-                        hd * 2, ctx, hipMemcpyHostToDevice));
-    HIP_TRY(hipMemcpy2D((uint16_t *)vc.ptr + (size_t)h * ctx * hd, hd * 2, vcache + (size_t)h * hd, (size_t)kv_dim * 2,
-                        hd * 2, ctx, hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy2D((uint16_t *)kc.ptr + (size_t)h * m.ctxp * hd, hd * 2, kcache + (size_t)h * hd,
+                        (size_t)kv_dim * 2, hd * 2, ctx, hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy2D(vstage.ptr, hd * 2, vcache + (size_t)h * hd, (size_t)kv_dim * 2, hd * 2, ctx,
+                        hipMemcpyHostToDevice));
+    HIP_TRY(launch_vt_copy((uint16_t *)vc.ptr + (size_t)h * hd * m.ctxp, (uint16_t *)vstage.ptr, hd, m.ctxp, 0, ctx,
+                           true, nullptr));
+    HIP_TRY(hipDeviceSynchronize());
   }
   std::vector<float> cosv((size_t)ctx * (hd / 2), 1.0f), sinv((size_t)ctx * (hd / 2), 0.0f);
   HIP_TRY(hipMemcpy(rc_.ptr, cosv.data(), cosv.size() * 4, hipMemcpyHostToDevice));
