@@ -220,8 +220,20 @@ struct ChunkTraits<FMT_F16> {
 template <int BS>
 __device__ inline void load_x_lds(const float *x, const float *normw, float eps, int K, float *xs, float *red) {
   if (!normw) {
-#pragma unroll 4
-    for (int i = 4 * threadIdx.x; i < K; i += 4 * BS) *(float4 *)(xs + i) = ld_coherent_f4(x, i);
+    // batches of 4 loads per thread, all issued before the first LDS write
+    for (int i0 = 4 * threadIdx.x; i0 < K; i0 += 16 * BS) {
+      float4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = i0 + u * 4 * BS;
+        v[u] = ld_coherent_f4(x, (unsigned)(i < K ? i : 0));
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = i0 + u * 4 * BS;
+        if (i < K) *(float4 *)(xs + i) = v[u];
+      }
+    }
     __syncthreads();
     return;
   }
@@ -243,21 +255,26 @@ __device__ inline void load_x_lds(const float *x, const float *normw, float eps,
     __syncthreads();
     return;
   }
-  // x and the norm weights are fetched together; the weights wait in registers
-  // (up to 4 float4 per thread) while the sum of squares is reduced.
+  // x and the norm weights are fetched together (all loads issued before the
+  // first use) and wait in registers (up to 4 float4 each per thread) while the
+  // sum of squares is reduced.
   float ss = 0.0f;
-  float4 wv[4];
+  float4 xv[4], wv[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int i = 4 * (threadIdx.x + u * BS);
+    const int ic = i < K ? i : 0;
+    xv[u] = ld_coherent_f4(x, (unsigned)ic);
+    wv[u] = *(const float4 *)(normw + ic);
+  }
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int i = 4 * (threadIdx.x + u * BS);
     if (i < K) {
-      float4 v = ld_coherent_f4(x, i);
-      wv[u] = *(const float4 *)(normw + i);
-      *(float4 *)(xs + i) = v;
-      ss += v.x * v.x;
-      ss += v.y * v.y;
-      ss += v.z * v.z;
-      ss += v.w * v.w;
+      ss += xv[u].x * xv[u].x;
+      ss += xv[u].y * xv[u].y;
+      ss += xv[u].z * xv[u].z;
+      ss += xv[u].w * xv[u].w;
     }
   }
   ss = block_sum<BS>(ss, red);
@@ -268,7 +285,7 @@ __device__ inline void load_x_lds(const float *x, const float *normw, float eps,
   for (int u = 0; u < 4; ++u) {
     const int i = 4 * (threadIdx.x + u * BS);
     if (i < K) {
-      float4 v = *(float4 *)(xs + i);
+      float4 v = xv[u];
       v.x = wv[u].x * (ss * v.x);
       v.y = wv[u].y * (ss * v.y);
       v.z = wv[u].z * (ss * v.z);
@@ -310,16 +327,50 @@ __device__ __forceinline__ void wait_vmem() {
 }
 __device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-// 16 (4) bytes per lane from rsrc + voff + soff into LDS at lds + 16 (4) * lane.
-#define GL3_DMA_NT 2  // cache policy: nontemporal (weights are read once per token)
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void *lds, unsigned voff, unsigned soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)lds, 16, voff, soff, 0, GL3_DMA_NT);
+// Buffer descriptor of a weight / cache region: base, stride 0, 2^31-1 bytes.
+typedef int dma_rsrc_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ dma_rsrc_t rsrc(const void *p) {
+  const unsigned long long b = (unsigned long long)p;
+  dma_rsrc_t r;
+  r.x = (int)(unsigned)b;
+  r.y = (int)((unsigned)(b >> 32) & 0xffffu);
+  r.z = 0x7fffffff;
+  r.w = 0x00020000;
+  return r;
 }
-__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, void *lds, unsigned voff, unsigned soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)lds, 4, voff, soff, 0, GL3_DMA_NT);
+
+// 16 (4) bytes per lane from rsrc + voff + soff into LDS at lds + 16 (4) * lane,
+// nontemporal (weights and KV are read once per token).  Written as inline
+// assembly on purpose: the compiler does not see these loads as LDS writes,
+// so it adds no waits of its own before LDS accesses; every read of a ring
+// slot is preceded by an explicit s_waitcnt on the loads issued for it, and
+// every reissue into a slot by s_waitcnt lgkmcnt(0) (its reads completed).
+// descriptor, LDS address and soffset are wave-uniform: read them from lane 0 into SGPRs
+__device__ __forceinline__ dma_rsrc_t uniform(dma_rsrc_t r) {
+  dma_rsrc_t u;
+  u.x = __builtin_amdgcn_readfirstlane(r.x);
+  u.y = __builtin_amdgcn_readfirstlane(r.y);
+  u.z = __builtin_amdgcn_readfirstlane(r.z);
+  u.w = __builtin_amdgcn_readfirstlane(r.w);
+  return u;
 }
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *p) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, 0x7fffffff, 0x00020000);
+__device__ __forceinline__ void dma16(dma_rsrc_t r, void *lds, unsigned voff, unsigned soff) {
+  r = uniform(r);
+  soff = __builtin_amdgcn_readfirstlane(soff);
+  const unsigned m0v = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(lds_void_t *)lds);
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen nt lds"
+               :
+               : "s"(m0v), "v"(voff), "s"(r), "s"(soff)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(dma_rsrc_t r, void *lds, unsigned voff, unsigned soff) {
+  r = uniform(r);
+  soff = __builtin_amdgcn_readfirstlane(soff);
+  const unsigned m0v = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(lds_void_t *)lds);
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen nt lds"
+               :
+               : "s"(m0v), "v"(voff), "s"(r), "s"(soff)
+               : "memory", "m0");
 }
 
 template <int FMT, int KC, int KS, int NR, int MODE, int BS, int SC_ = 0, int DEPTH = 2>
@@ -371,7 +422,7 @@ struct GemvPhase {
     const int item = blk + (u / PASSES) * nblk, pass = PASSES > 1 ? u % PASSES : 0;
     const int j0 = pass * JP;
     u32x4 *rw = ring_w<S, WCH>() + wave * SC * GL3_WAVE;
-    const __amdgpu_buffer_rsrc_t rq = rsrc(W.q);
+    const dma_rsrc_t rq = rsrc(W.q);
     wait_lds();  // reads of the slot's previous contents have completed
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
@@ -392,7 +443,7 @@ struct GemvPhase {
       constexpr int TOTAL = NR * NP * SEG;
       const int valid = (PASSES > 1 && KC - j0 < JP) ? (KC - j0) * 64 : SEG;
       unsigned *rs = ring_s<S, SDW>() + wave * SC * 16;
-      const __amdgpu_buffer_rsrc_t rsc = rsrc(W.s);
+      const dma_rsrc_t rsc = rsrc(W.s);
 #pragma unroll
       for (int i = 0; i < NSI; ++i) {
         int b = 256 * i + 4 * lane;
@@ -749,16 +800,168 @@ __device__ __forceinline__ float inv_rms(float ss, int hd, float eps) {
   return (float)(1.0 / sqrt((double)ss));
 }
 
+// One wave's share of a (kv head, split) item: tile DMA and tile compute.  The
+// ring slot is a template parameter so that each slot is its own LDS object and
+// the compiler's own wait counts do not serialize the slots.
+template <int HD, int GQ>
+struct AttTile {
+  static constexpr int NQ = HD / 8, NC = HD / 32, NB = HD / 16, NKI = HD / 32, NVI = HD / 32, NI = NKI + NVI;
+  static constexpr int KT_U4 = 16 * NQ;
+  const ModelDev *m;
+  dma_rsrc_t rk, rv;
+  int t0, t1, pos, wave, lane;
+
+  template <int S>
+  __device__ __forceinline__ u32x4 *slot() const {
+    return ring_w<S, ATT_RING_U4>() + wave * 8 * GL3_WAVE;
+  }
+
+  // DMA of this wave's u-th tile (positions t0 + 16 (wave + 4u) ..) into ring slot S
+  template <int S>
+  __device__ __forceinline__ void issue(int u) const {
+    const int t = t0 + 16 * (wave + 4 * u);
+    u32x4 *sl = slot<S>();
+    wait_lds();
+#pragma unroll
+    for (int i = 0; i < NKI; ++i) {
+      const int ci = GL3_WAVE * i + lane, p = ci / NQ;
+      int q = ci % NQ - kswz<NQ>(p);
+      q = q < 0 ? q + NQ : q;
+      dma16(rk, sl + GL3_WAVE * i, (unsigned)(((t + p) * HD + 8 * q) * 2), 0u);
+    }
+#pragma unroll
+    for (int i = 0; i < NVI; ++i) {
+      const int d = 32 * i + lane / 2;
+      dma16(rv, sl + KT_U4 + GL3_WAVE * i, (unsigned)((d * m->ctxp + t + 8 * (lane % 2)) * 2), 0u);
+    }
+  }
+
+  template <int S>
+  __device__ __forceinline__ void step(int u, int ntw, const half8 (&qh)[NC], const half8 (&ql)[NC],
+                                       const unsigned (&knb)[4], const unsigned (&vnb)[4], f32x4 (&O)[NB],
+                                       float &mrun, float &lrun) const {
+    if (u >= ntw) return;
+    // slot S is complete once at most the loads of the later issued tiles are outstanding
+    const int later = ntw - 1 - u;
+    if (later >= 2)
+      wait_vmem<2 * NI>();
+    else if (later == 1)
+      wait_vmem<NI>();
+    else
+      wait_vmem<0>();
+    tile<S>(u, qh, ql, knb, vnb, O, mrun, lrun);
+    if (u + ATT_DEPTH < ntw) issue<S>(u + ATT_DEPTH);
+  }
+
+  template <int S>
+  __device__ __forceinline__ void tile(int u, const half8 (&qh)[NC], const half8 (&ql)[NC], const unsigned (&knb)[4],
+                                       const unsigned (&vnb)[4], f32x4 (&O)[NB], float &mrun, float &lrun) const {
+    u32x4 *sl = slot<S>();
+    const int hh = lane % 16, kb = lane / 16;
+    const int t = t0 + 16 * (wave + 4 * u);
+    const int nvalid = min(16, t1 - t);
+    // The row of the new position is stale in the tile (the DMA may have read
+    // the cache before the append): its K chunk and V entries are replaced in
+    // registers from the lanes holding the new k, v (lane i: dims 8i..8i+7).
+    // The tile is only read, never written, so the slots stay independent.
+    const bool has_pos = pos >= t && pos < t + 16;
+    const int pl = pos - t;
+    // scores S[pos][head] = K . Q^T
+    f32x4 sacc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int p = hh, q = 4 * c + kb;
+      u32x4 kw = sl[p * NQ + (q + kswz<NQ>(p)) % NQ];
+      if (has_pos) {
+        const u32x4 kn = u32x4{(unsigned)__shfl((int)knb[0], q), (unsigned)__shfl((int)knb[1], q),
+                               (unsigned)__shfl((int)knb[2], q), (unsigned)__shfl((int)knb[3], q)};
+        if (p == pl) kw = kn;
+      }
+      const half8 a = __builtin_bit_cast(half8, kw);
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[c], sacc, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[c], sacc, 0, 0, 0);
+    }
+    // lane: head hh, positions 4*kb + v
+    float sv[4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const bool ok = hh < GQ && 4 * kb + v < nvalid;
+      sv[v] = ok ? sacc[v] / m->sqrt_hd : -INFINITY;
+      mx = fmaxf(mx, sv[v]);
+    }
+    mx = xrow_max(mx);
+    const float mn = fmaxf(mrun, mx);
+    const float cf = (mrun == -INFINITY) ? 0.0f : __expf(mrun - mn);
+    float p4[4], ls = 0.0f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      p4[v] = (sv[v] == -INFINITY) ? 0.0f : __expf(sv[v] - mn);
+      ls += p4[v];
+    }
+    ls = xrow_sum(ls);
+    if (mn != -INFINITY) {
+      lrun = lrun * cf + ls;
+      mrun = mn;
+    }
+    // O rows are heads 4*kb + v (kb < 2 for GQ <= 8): their rescale factors
+    // live in lanes 4*kb + v; rows of heads >= GQ hold zeros
+    float cr[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float cv = readlane_f(cf, v), mv = readlane_f(mn, v);
+      if (GQ > 4 && kb == 1) {
+        cv = readlane_f(cf, 4 + v);
+        mv = readlane_f(mn, 4 + v);
+      }
+      cr[v] = (mv == -INFINITY) ? 1.0f : cv;
+    }
+    half4 ph, plo;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const _Float16 h16 = (_Float16)p4[v];
+      ph[v] = h16;
+      plo[v] = (_Float16)(p4[v] - (float)h16);
+    }
+    const uint2 *vt2 = (const uint2 *)(sl + KT_U4);
+    // positions >= nvalid of a partial tile read zeros (p is 0 there too)
+    const unsigned keep0 = (4 * kb + 0 < nvalid ? 0x0000ffffu : 0u) | (4 * kb + 1 < nvalid ? 0xffff0000u : 0u);
+    const unsigned keep1 = (4 * kb + 2 < nvalid ? 0x0000ffffu : 0u) | (4 * kb + 3 < nvalid ? 0xffff0000u : 0u);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) O[b][v] *= cr[v];
+      uint2 w = vt2[(16 * b + hh) * 4 + kb];  // V^T row 16b+hh, positions 4kb..4kb+3
+      if (has_pos) {
+        const int d = 16 * b + hh, src = d / 8;  // the new v of dim d: lane d/8, element d%8
+        const unsigned w0 = (unsigned)__shfl((int)vnb[0], src), w1 = (unsigned)__shfl((int)vnb[1], src);
+        const unsigned w2 = (unsigned)__shfl((int)vnb[2], src), w3 = (unsigned)__shfl((int)vnb[3], src);
+        const int e = d % 8;
+        const unsigned word = e < 2 ? w0 : (e < 4 ? w1 : (e < 6 ? w2 : w3));
+        const unsigned h16 = (word >> (16 * (e % 2))) & 0xffffu;
+        if (pl / 4 == kb) {
+          const int j = pl % 4;
+          if (j == 0) w.x = (w.x & 0xffff0000u) | h16;
+          if (j == 1) w.x = (w.x & 0x0000ffffu) | (h16 << 16);
+          if (j == 2) w.y = (w.y & 0xffff0000u) | h16;
+          if (j == 3) w.y = (w.y & 0x0000ffffu) | (h16 << 16);
+        }
+      }
+      w.x &= keep0;
+      w.y &= keep1;
+      const half4 vb = __builtin_bit_cast(half4, w);
+      O[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, vb, O[b], 0, 0, 0);
+      O[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(plo, vb, O[b], 0, 0, 0);
+    }
+  }
+};
+
 template <int HD, int GQ, int BS>
 __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, int nblk, float *lds) {
   constexpr int WPB = BS / GL3_WAVE;
   constexpr int NQ = HD / 8;           // 16-byte chunks of a K row
   constexpr int NC = HD / 32;          // 32-dim chunks (score MFMAs per tile and hi/lo)
   constexpr int NB = HD / 16;          // 16-dim blocks of the output
-  constexpr int NKI = HD / 32;         // DMA loads of a K tile (16 rows x HD x 2 B = NKI KB)
-  constexpr int NVI = HD / 32;         // DMA loads of a V tile
-  constexpr int NI = NKI + NVI;
-  constexpr int KT_U4 = 16 * NQ;       // K tile size in u32x4
   static_assert(WPB == 4 && HD % 32 == 0 && HD <= 128 && GQ <= 8, "attention tile shape");
   const int hd = HD, half = HD / 2;
   const int n = pos + 1;
@@ -773,9 +976,6 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
   const int wave = wave_id(), lane = lane_id();
   const int hh = lane % 16, kb = lane / 16;  // MFMA column (head) and k-block of this lane
   const bool neox = m.family != FAM_LLAMA, qwen = m.family == FAM_QWEN3;
-  u32x4 *ring0 = ring_w<0, ATT_RING_U4>() + wave * 8 * GL3_WAVE;
-  u32x4 *ring1 = ring_w<1, ATT_RING_U4>() + wave * 8 * GL3_WAVE;
-  u32x4 *ring2 = ring_w<2, ATT_RING_U4>() + wave * 8 * GL3_WAVE;
 
   for (int item = blk; item < items; item += nblk) {
     const int kvh = item / nsplit, sp = item % nsplit;
@@ -785,28 +985,20 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
     const int ntw = wave < ntile ? (ntile - 1 - wave) / WPB + 1 : 0;  // tiles of this wave
     uint16_t *kbase = m.kc + ((size_t)layer * m.n_kv + kvh) * m.ctxp * HD;
     uint16_t *vbase = m.vc + ((size_t)layer * m.n_kv + kvh) * HD * m.ctxp;
-    const __amdgpu_buffer_rsrc_t rk = rsrc(kbase), rv = rsrc(vbase);
+    const dma_rsrc_t rk = rsrc(kbase), rv = rsrc(vbase);
 
-    // DMA of this wave's u-th tile into ring slot `slot`
-    auto issue = [&](u32x4 *slot, int u) __attribute__((always_inline)) {
-      const int t = t0 + 16 * (wave + WPB * u);
-      wait_lds();
-#pragma unroll
-      for (int i = 0; i < NKI; ++i) {
-        const int ci = GL3_WAVE * i + lane, p = ci / NQ;
-        int q = ci % NQ - kswz<NQ>(p);
-        q = q < 0 ? q + NQ : q;
-        dma16(rk, slot + GL3_WAVE * i, (unsigned)(((t + p) * HD + 8 * q) * 2), 0u);
-      }
-#pragma unroll
-      for (int i = 0; i < NVI; ++i) {
-        const int d = 32 * i + lane / 2;
-        dma16(rv, slot + KT_U4 + GL3_WAVE * i, (unsigned)((d * m.ctxp + t + 8 * (lane % 2)) * 2), 0u);
-      }
-    };
-    if (ntw > 0) issue(ring0, 0);
-    if (ntw > 1) issue(ring1, 1);
-    if (ntw > 2) issue(ring2, 2);
+    AttTile<HD, GQ> at;
+    at.m = &m;
+    at.rk = rk;
+    at.rv = rv;
+    at.t0 = t0;
+    at.t1 = t1;
+    at.pos = pos;
+    at.wave = wave;
+    at.lane = lane;
+    if (ntw > 0) at.template issue<0>(0);
+    if (ntw > 1) at.template issue<1>(1);
+    if (ntw > 2) at.template issue<2>(2);
 
     // ---- q of head hh (columns >= GQ stay zero), the new k and v: one round trip
     float qv[NC][8];
@@ -838,9 +1030,7 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
         }
       }
       if (qwen) {
-        ss += __shfl_xor(ss, 16);
-        ss += __shfl_xor(ss, 32);
-        const float si = inv_rms(ss, hd, m.eps);
+        const float si = inv_rms(xrow_sum(ss), hd, m.eps);
 #pragma unroll
         for (int c = 0; c < NC; ++c)
 #pragma unroll
@@ -941,100 +1131,10 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
 #pragma unroll
     for (int b = 0; b < NB; ++b) O[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     float mrun = -INFINITY, lrun = 0.0f;
-    auto tile = [&](u32x4 *slot, int u) __attribute__((always_inline)) {
-      const int t = t0 + 16 * (wave + WPB * u);
-      const int nvalid = min(16, t1 - t);
-      // the new position and the tail of a partial tile are written into the LDS tile
-      if (pos >= t && pos < t + 16) {
-        const int pl = pos - t;
-        if (lane < NQ) {
-          slot[pl * NQ + (lane + kswz<NQ>(pl)) % NQ] = u32x4{knb[0], knb[1], knb[2], knb[3]};
-          uint16_t *vt = (uint16_t *)(slot + KT_U4);
-#pragma unroll
-          for (int i = 0; i < 8; ++i) vt[(8 * lane + i) * 16 + pl] = (uint16_t)(vnb[i / 2] >> (16 * (i % 2)));
-        }
-      }
-      if (nvalid < 16) {
-        uint16_t *vt = (uint16_t *)(slot + KT_U4);
-        for (int idx = lane; idx < HD * 16; idx += GL3_WAVE)
-          if (idx % 16 >= nvalid) vt[idx] = 0;
-      }
-      // scores
-      f32x4 sacc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const int p = hh, q = 4 * c + kb;
-        const u32x4 w = slot[p * NQ + (q + kswz<NQ>(p)) % NQ];
-        const half8 a = __builtin_bit_cast(half8, w);
-        sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[c], sacc, 0, 0, 0);
-        sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[c], sacc, 0, 0, 0);
-      }
-      // lane: head hh, positions 4*kb + v
-      float sv[4];
-      float mx = -INFINITY;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const bool ok = hh < GQ && 4 * kb + v < nvalid;
-        sv[v] = ok ? sacc[v] / m.sqrt_hd : -INFINITY;
-        mx = fmaxf(mx, sv[v]);
-      }
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float mn = fmaxf(mrun, mx);
-      const float cf = (mrun == -INFINITY) ? 0.0f : __expf(mrun - mn);
-      float p4[4], ls = 0.0f;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        p4[v] = (sv[v] == -INFINITY) ? 0.0f : __expf(sv[v] - mn);
-        ls += p4[v];
-      }
-      ls += __shfl_xor(ls, 16);
-      ls += __shfl_xor(ls, 32);
-      if (mn != -INFINITY) {
-        lrun = lrun * cf + ls;
-        mrun = mn;
-      }
-      // O rows are heads 4*kb + v: their rescale factors live in lanes 4*kb + v
-      float cr[4];
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const float cv = __shfl(cf, 4 * kb + v);
-        const float mv = __shfl(mn, 4 * kb + v);
-        cr[v] = (mv == -INFINITY) ? 1.0f : cv;
-      }
-      half4 ph, pl;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const _Float16 h16 = (_Float16)p4[v];
-        ph[v] = h16;
-        pl[v] = (_Float16)(p4[v] - (float)h16);
-      }
-      const uint2 *vt2 = (const uint2 *)(slot + KT_U4);
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) O[b][v] *= cr[v];
-        const uint2 w = vt2[(16 * b + hh) * 4 + kb];  // V^T row 16b+hh, positions 4kb..4kb+3
-        const half4 vb = __builtin_bit_cast(half4, w);
-        O[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, vb, O[b], 0, 0, 0);
-        O[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, vb, O[b], 0, 0, 0);
-      }
-    };
     for (int u = 0; u < ntw; u += ATT_DEPTH) {
-      // slot s is complete once at most the loads of the later issued tiles are outstanding
-#define GL3_ATT_STEP(SLOT, K)                                                       \
-      if (u + K < ntw) {                                                            \
-        const int later = ntw - 1 - (u + K);                                        \
-        if (later >= 2) wait_vmem<2 * NI>();                                        \
-        else if (later == 1) wait_vmem<NI>();                                       \
-        else wait_vmem<0>();                                                        \
-        tile(SLOT, u + K);                                                          \
-        if (u + K + ATT_DEPTH < ntw) issue(SLOT, u + K + ATT_DEPTH);                \
-      }
-      GL3_ATT_STEP(ring0, 0)
-      GL3_ATT_STEP(ring1, 1)
-      GL3_ATT_STEP(ring2, 2)
-#undef GL3_ATT_STEP
+      at.template step<0>(u, ntw, qh, ql, knb, vnb, O, mrun, lrun);
+      at.template step<1>(u + 1, ntw, qh, ql, knb, vnb, O, mrun, lrun);
+      at.template step<2>(u + 2, ntw, qh, ql, knb, vnb, O, mrun, lrun);
     }
     // ---- wave partials to LDS: O rows (heads) 4*kb + v, columns (dims) 16b + hh
 #pragma unroll
@@ -1132,12 +1232,11 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
         for (int s0 = q; s0 < nsplit; s0 += 8 * nt) {
           float4 hv[8], ov[8];
 #pragma unroll
-          for (int b = 0; b < 8; ++b) {
+          for (int b = 0; b < 8; ++b) {  // all 16 loads in flight together
             const int s = s0 + b * nt;
-            if (s < nsplit) {
-              hv[b] = ld_coherent_f4(base, (unsigned)(s * hpart + hd));
-              ov[b] = ld_coherent_f4(base, (unsigned)(s * hpart + dd));
-            }
+            const int sc = s < nsplit ? s : 0;
+            hv[b] = ld_coherent_f4(base, (unsigned)(sc * hpart + hd));
+            ov[b] = ld_coherent_f4(base, (unsigned)(sc * hpart + dd));
           }
 #pragma unroll
           for (int b = 0; b < 8; ++b) {
