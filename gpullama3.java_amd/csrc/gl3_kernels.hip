@@ -348,17 +348,30 @@ __global__ void fill_normal_f16_kernel(uint16_t *dst, size_t rows, size_t cols, 
   }
 }
 
-// V cache <-> position-major rows: vt is one kv head's [hd][ctxp] block, rows is
-// [npos][hd] (positions pos0..pos0+npos-1)
-__global__ void vt_copy_kernel(uint16_t *vt, uint16_t *rows, int hd, int ctxp, int pos0, int npos, int to_vt) {
+// V cache <-> position-major rows: vt is one kv head's [ctxp/16][hd][16] region,
+// rows is [npos][hd] (positions pos0..pos0+npos-1)
+__device__ __forceinline__ size_t vt_index(int t, int d, int hd) { return ((size_t)(t / 16) * hd + d) * 16 + t % 16; }
+__global__ void vt_copy_kernel(uint16_t *vt, uint16_t *rows, int hd, int pos0, int npos, int to_vt) {
   const size_t n = (size_t)npos * hd;
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
     const int t = (int)(i / hd), d = (int)(i % hd);
-    uint16_t *v = vt + (size_t)d * ctxp + pos0 + t;
+    uint16_t *v = vt + vt_index(pos0 + t, d, hd);
     if (to_vt)
       *v = rows[i];
     else
       rows[i] = *v;
+  }
+}
+// N(0,1) history for positions 0..npos-1 of one kv head's V region (draw d * npos + t)
+__global__ void fill_normal_vt_kernel(uint16_t *vt, int hd, int npos, unsigned long long seed) {
+  const size_t n = (size_t)npos * hd;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    const int d = (int)(i / npos), t = (int)(i % npos);
+    unsigned long long h = splitmix64(seed ^ splitmix64(i));
+    float u1 = ((float)(h >> 40) + 0.5f) * (1.0f / 16777216.0f);
+    float u2 = (float)((h >> 16) & 0xFFFFFFull) * (1.0f / 16777216.0f);
+    float r = sqrtf(-2.0f * logf(u1));
+    vt[vt_index(t, d, hd)] = f2h(r * cospif(2.0f * u2));
   }
 }
 
@@ -391,13 +404,18 @@ hipError_t launch_fill_normal_f16(uint16_t *dst, size_t rows, size_t cols, size_
   hipLaunchKernelGGL(fill_normal_f16_kernel, dim3((unsigned)grid), dim3(256), 0, st, dst, rows, cols, stride, seed);
   return hipGetLastError();
 }
-hipError_t launch_vt_copy(uint16_t *vt, uint16_t *rows, int hd, int ctxp, int pos0, int npos, bool to_vt,
-                          hipStream_t st) {
+hipError_t launch_vt_copy(uint16_t *vt, uint16_t *rows, int hd, int pos0, int npos, bool to_vt, hipStream_t st) {
   size_t grid = ((size_t)npos * hd + 255) / 256;
   if (grid > 65536) grid = 65536;
   if (grid == 0) grid = 1;
-  hipLaunchKernelGGL(vt_copy_kernel, dim3((unsigned)grid), dim3(256), 0, st, vt, rows, hd, ctxp, pos0, npos,
-                     to_vt ? 1 : 0);
+  hipLaunchKernelGGL(vt_copy_kernel, dim3((unsigned)grid), dim3(256), 0, st, vt, rows, hd, pos0, npos, to_vt ? 1 : 0);
+  return hipGetLastError();
+}
+hipError_t launch_fill_normal_vt(uint16_t *vt, int hd, int npos, unsigned long long seed, hipStream_t st) {
+  size_t grid = ((size_t)npos * hd + 255) / 256;
+  if (grid > 65536) grid = 65536;
+  if (grid == 0) grid = 1;
+  hipLaunchKernelGGL(fill_normal_vt_kernel, dim3((unsigned)grid), dim3(256), 0, st, vt, hd, npos, seed);
   return hipGetLastError();
 }
 

@@ -84,7 +84,7 @@ struct ModelDev {
   const float *out_norm;
   const float *rope_cos, *rope_sin;  // [ctx][hd/2]
   uint16_t *kc;             // fp16 K cache [L][n_kv][ctxp][hd]
-  uint16_t *vc;             // fp16 V cache, transposed: [L][n_kv][hd][ctxp]
+  uint16_t *vc;             // fp16 V cache in 16-position blocks, transposed: [L][n_kv][ctxp/16][hd][16]
   float *x;                 // residual stream [dim]
   float *qkv;               // raw q,k,v [q_dim + 2 kv_dim]
   float *att;               // attention output [q_dim]
@@ -700,9 +700,9 @@ struct GemvPhase {
 //
 // The split is cut into tiles of 16 positions; wave w takes tiles w, w+4, ...
 // A tile's K rows ([16][hd], contiguous in the cache) and V columns (the V
-// cache is stored transposed, [hd][ctxp], so 16 positions of one dimension are
-// contiguous) stream into the per-wave LDS ring of the GEMV phases by DMA,
-// DEPTH tiles ahead.  Per tile:
+// cache is stored in 16-position blocks, each transposed to [hd][16], so a
+// tile's V is one contiguous 2*16*hd-byte block) stream into the per-wave LDS
+// ring of the GEMV phases by DMA, DEPTH tiles ahead.  Per tile:
 //   S[16 pos][16 heads] = K[16][hd] . Q^T    v_mfma_f32_16x16x32_f16
 //   online softmax over the tile (scores / sqrt(hd), InferenceCore.java:114-121)
 //   O[16 heads][hd]    += P[16][16] . V     v_mfma_f32_16x16x16_f16
@@ -832,7 +832,7 @@ struct AttTile {
 #pragma unroll
     for (int i = 0; i < NVI; ++i) {
       const int d = 32 * i + lane / 2;
-      dma16(rv, sl + KT_U4 + GL3_WAVE * i, (unsigned)((d * m->ctxp + t + 8 * (lane % 2)) * 2), 0u);
+      dma16(rv, sl + KT_U4 + GL3_WAVE * i, (unsigned)((t * HD + 16 * d + 8 * (lane % 2)) * 2), 0u);
     }
   }
 
@@ -860,24 +860,53 @@ struct AttTile {
     const int hh = lane % 16, kb = lane / 16;
     const int t = t0 + 16 * (wave + 4 * u);
     const int nvalid = min(16, t1 - t);
+    // all LDS reads of the tile first: K chunks (MFMA A operand: row hh, dims
+    // 32c + 8kb..) and V^T rows 16b + hh, positions 4kb..4kb+3 (B operand)
+    u32x4 kw[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int q = 4 * c + kb;
+      kw[c] = sl[hh * NQ + (q + kswz<NQ>(hh)) % NQ];
+    }
+    const uint2 *vt2 = (const uint2 *)(sl + KT_U4);
+    uint2 vw[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) vw[b] = vt2[(16 * b + hh) * 4 + kb];
     // The row of the new position is stale in the tile (the DMA may have read
-    // the cache before the append): its K chunk and V entries are replaced in
+    // the cache before the append): its K chunks and V entries are replaced in
     // registers from the lanes holding the new k, v (lane i: dims 8i..8i+7).
     // The tile is only read, never written, so the slots stay independent.
-    const bool has_pos = pos >= t && pos < t + 16;
-    const int pl = pos - t;
+    if (__builtin_expect(pos >= t && pos < t + 16, 0)) {
+      const int pl = pos - t;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int q = 4 * c + kb;
+        const u32x4 kn = u32x4{(unsigned)__shfl((int)knb[0], q), (unsigned)__shfl((int)knb[1], q),
+                               (unsigned)__shfl((int)knb[2], q), (unsigned)__shfl((int)knb[3], q)};
+        if (hh == pl) kw[c] = kn;
+      }
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const int d = 16 * b + hh, src = d / 8;  // the new v of dim d: lane d/8, element d%8
+        const unsigned w0 = (unsigned)__shfl((int)vnb[0], src), w1 = (unsigned)__shfl((int)vnb[1], src);
+        const unsigned w2 = (unsigned)__shfl((int)vnb[2], src), w3 = (unsigned)__shfl((int)vnb[3], src);
+        const int e = d % 8;
+        const unsigned word = e < 2 ? w0 : (e < 4 ? w1 : (e < 6 ? w2 : w3));
+        const unsigned h16 = (word >> (16 * (e % 2))) & 0xffffu;
+        if (pl / 4 == kb) {
+          const int j = pl % 4;
+          if (j == 0) vw[b].x = (vw[b].x & 0xffff0000u) | h16;
+          if (j == 1) vw[b].x = (vw[b].x & 0x0000ffffu) | (h16 << 16);
+          if (j == 2) vw[b].y = (vw[b].y & 0xffff0000u) | h16;
+          if (j == 3) vw[b].y = (vw[b].y & 0x0000ffffu) | (h16 << 16);
+        }
+      }
+    }
     // scores S[pos][head] = K . Q^T
     f32x4 sacc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const int p = hh, q = 4 * c + kb;
-      u32x4 kw = sl[p * NQ + (q + kswz<NQ>(p)) % NQ];
-      if (has_pos) {
-        const u32x4 kn = u32x4{(unsigned)__shfl((int)knb[0], q), (unsigned)__shfl((int)knb[1], q),
-                               (unsigned)__shfl((int)knb[2], q), (unsigned)__shfl((int)knb[3], q)};
-        if (p == pl) kw = kn;
-      }
-      const half8 a = __builtin_bit_cast(half8, kw);
+      const half8 a = __builtin_bit_cast(half8, kw[c]);
       sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[c], sacc, 0, 0, 0);
       sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[c], sacc, 0, 0, 0);
     }
@@ -923,7 +952,6 @@ struct AttTile {
       ph[v] = h16;
       plo[v] = (_Float16)(p4[v] - (float)h16);
     }
-    const uint2 *vt2 = (const uint2 *)(sl + KT_U4);
     // positions >= nvalid of a partial tile read zeros (p is 0 there too)
     const unsigned keep0 = (4 * kb + 0 < nvalid ? 0x0000ffffu : 0u) | (4 * kb + 1 < nvalid ? 0xffff0000u : 0u);
     const unsigned keep1 = (4 * kb + 2 < nvalid ? 0x0000ffffu : 0u) | (4 * kb + 3 < nvalid ? 0xffff0000u : 0u);
@@ -931,22 +959,7 @@ struct AttTile {
     for (int b = 0; b < NB; ++b) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) O[b][v] *= cr[v];
-      uint2 w = vt2[(16 * b + hh) * 4 + kb];  // V^T row 16b+hh, positions 4kb..4kb+3
-      if (has_pos) {
-        const int d = 16 * b + hh, src = d / 8;  // the new v of dim d: lane d/8, element d%8
-        const unsigned w0 = (unsigned)__shfl((int)vnb[0], src), w1 = (unsigned)__shfl((int)vnb[1], src);
-        const unsigned w2 = (unsigned)__shfl((int)vnb[2], src), w3 = (unsigned)__shfl((int)vnb[3], src);
-        const int e = d % 8;
-        const unsigned word = e < 2 ? w0 : (e < 4 ? w1 : (e < 6 ? w2 : w3));
-        const unsigned h16 = (word >> (16 * (e % 2))) & 0xffffu;
-        if (pl / 4 == kb) {
-          const int j = pl % 4;
-          if (j == 0) w.x = (w.x & 0xffff0000u) | h16;
-          if (j == 1) w.x = (w.x & 0x0000ffffu) | (h16 << 16);
-          if (j == 2) w.y = (w.y & 0xffff0000u) | h16;
-          if (j == 3) w.y = (w.y & 0x0000ffffu) | (h16 << 16);
-        }
-      }
+      uint2 w = vw[b];
       w.x &= keep0;
       w.y &= keep1;
       const half4 vb = __builtin_bit_cast(half4, w);
@@ -1122,7 +1135,7 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
         *(u32x4 *)(kbase + (size_t)pos * HD + d0) = u32x4{knb[0], knb[1], knb[2], knb[3]};
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-          vbase[(size_t)(d0 + i) * m.ctxp + pos] = (uint16_t)(vnb[i / 2] >> (16 * (i % 2)));
+          vbase[(size_t)(pos / 16) * 16 * HD + (d0 + i) * 16 + pos % 16] = (uint16_t)(vnb[i / 2] >> (16 * (i % 2)));
       }
     }
 

@@ -749,7 +749,7 @@ extern "C" int gl3_reset(gl3_plan *p) {
   return GL3_OK;
 }
 
-// KV cache: device K [L][n_kv][ctxp][hd] and V [L][n_kv][hd][ctxp]; host [npos][n_kv*hd]
+// KV cache: device K [L][n_kv][ctxp][hd] and V [L][n_kv][ctxp/16][hd][16]; host [npos][n_kv*hd]
 static int kv_copy(gl3_plan *p, int layer, int pos0, int npos, uint16_t *host_k, uint16_t *host_v, bool to_device) {
   const gl3_config &c = p->cfg;
   if (layer < 0 || layer >= c.n_layers || pos0 < 0 || npos < 0 || (int64_t)pos0 + npos > c.context_length)
@@ -769,10 +769,10 @@ static int kv_copy(gl3_plan *p, int layer, int pos0, int npos, uint16_t *host_k,
     if (to_device) {
       he = hipMemcpy2DAsync(kdev, hd * 2, hk, (size_t)p->kv_dim * 2, hd * 2, npos, kind, p->stream);
       if (he == hipSuccess) he = hipMemcpy2DAsync(stage, hd * 2, hv, (size_t)p->kv_dim * 2, hd * 2, npos, kind, p->stream);
-      if (he == hipSuccess) he = launch_vt_copy(vt, stage, hd, ctxp, pos0, npos, true, p->stream);
+      if (he == hipSuccess) he = launch_vt_copy(vt, stage, hd, pos0, npos, true, p->stream);
     } else {
       he = hipMemcpy2DAsync(hk, (size_t)p->kv_dim * 2, kdev, hd * 2, hd * 2, npos, kind, p->stream);
-      if (he == hipSuccess) he = launch_vt_copy(vt, stage, hd, ctxp, pos0, npos, false, p->stream);
+      if (he == hipSuccess) he = launch_vt_copy(vt, stage, hd, pos0, npos, false, p->stream);
       if (he == hipSuccess) he = hipMemcpy2DAsync(hv, (size_t)p->kv_dim * 2, stage, hd * 2, hd * 2, npos, kind, p->stream);
     }
     if (he == hipSuccess) he = hipStreamSynchronize(p->stream);  // the staging buffer is reused per head
@@ -803,8 +803,7 @@ extern "C" int gl3_fill_kv_normal(gl3_plan *p, uint64_t seed, int npos) {
       const size_t head = (size_t)l * c.n_kv_heads + h;
       unsigned long long sk = seed ^ (0x100000001B3ull * (unsigned long long)(2 * head + 1));
       HIP_TRY(launch_fill_normal_f16(p->m.kc + head * ctxp * hd, 1, (size_t)npos * hd, 0, sk, p->stream));
-      HIP_TRY(launch_fill_normal_f16(p->m.vc + head * hd * ctxp, hd, (size_t)npos, ctxp, sk ^ 0xA5A5A5A5A5A5A5A5ull,
-                                     p->stream));
+      HIP_TRY(launch_fill_normal_vt(p->m.vc + head * hd * ctxp, (int)hd, npos, sk ^ 0xA5A5A5A5A5A5A5A5ull, p->stream));
     }
   HIP_TRY(hipStreamSynchronize(p->stream));
   return GL3_OK;
@@ -974,14 +973,14 @@ extern "C" int gl3_op_attention(const float *q, const uint16_t *kcache, const ui
   DEV_ALLOC(st, sizeof(DecodeState));
   LayerDev L{};
   HIP_TRY(hipMemcpy(layers.ptr, &L, sizeof L, hipMemcpyHostToDevice));
-  // cache [pos+1][n_kv][hd] (host) -> K [n_kv][ctxp][hd], V [n_kv][hd][ctxp] (device)
+  // cache [pos+1][n_kv][hd] (host) -> K [n_kv][ctxp][hd], V [n_kv][ctxp/16][hd][16] (device)
   for (int h = 0; h < n_kv_heads; ++h) {
     HIP_TRY(hipMemcpy2D((uint16_t *)kc.ptr + (size_t)h * m.ctxp * hd, hd * 2, kcache + (size_t)h * hd,
                         (size_t)kv_dim * 2, hd * 2, ctx, hipMemcpyHostToDevice));
     HIP_TRY(hipMemcpy2D(vstage.ptr, hd * 2, vcache + (size_t)h * hd, (size_t)kv_dim * 2, hd * 2, ctx,
                         hipMemcpyHostToDevice));
-    HIP_TRY(launch_vt_copy((uint16_t *)vc.ptr + (size_t)h * hd * m.ctxp, (uint16_t *)vstage.ptr, hd, m.ctxp, 0, ctx,
-                           true, nullptr));
+    HIP_TRY(launch_vt_copy((uint16_t *)vc.ptr + (size_t)h * hd * m.ctxp, (uint16_t *)vstage.ptr, hd, 0, ctx, true,
+                           nullptr));
     HIP_TRY(hipDeviceSynchronize());
   }
   std::vector<float> cosv((size_t)ctx * (hd / 2), 1.0f), sinv((size_t)ctx * (hd / 2), 0.0f);
