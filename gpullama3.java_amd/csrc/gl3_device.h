@@ -164,19 +164,20 @@ __device__ __forceinline__ float group_sum(float v) {
 // ------------------------------------------------------------ grid barrier
 // Fence-free barrier for the persistent kernel (all workgroups co-resident,
 // guaranteed by the cooperative launch).  Workgroup b arrives on counter
-// b % 8 with a no-return atomic; wave 0 then polls the eight counters in
-// parallel.  Counters only grow: the barrier with global index e (across all
+// b % 64 with a no-return atomic (few arrivals per address); wave 0 then polls
+// the 64 counters, one per lane, in parallel.  Counters only grow: the barrier with global index e (across all
 // launches since the last reset) completes when counter j reaches
 // e * size_of_group(j).  Each poll is bounded: after spin_limit polls the
 // barrier raises *err and every workgroup leaves the kernel at its next
 // barrier, so a lost workgroup can never hang the GPU.
 struct GridBarrier {
-  unsigned *ctr;     // 8 counters, 64 words apart
+  unsigned *ctr;     // GL3_BAR_GROUPS counters, GL3_BAR_STRIDE words apart
   unsigned *err;     // error flag (0 = ok)
   unsigned spin_limit;
 };
 
-#define GL3_BAR_STRIDE 64
+#define GL3_BAR_STRIDE 64  // words between counters (one cache line each)
+#define GL3_BAR_GROUPS 64  // counters; workgroup b arrives on counter b % 64
 
 // Arrival: this workgroup's earlier writes are complete, then one no-return
 // atomic on its group counter.  Loads issued between grid_arrive and grid_wait
@@ -185,7 +186,8 @@ __device__ __forceinline__ void grid_arrive(const GridBarrier &gb) {
   vmem_drain();
   __syncthreads();
   if (threadIdx.x == 0)
-    __hip_atomic_fetch_add(gb.ctr + (blockIdx.x & 7u) * GL3_BAR_STRIDE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_fetch_add(gb.ctr + (blockIdx.x % GL3_BAR_GROUPS) * GL3_BAR_STRIDE, 1u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Waits until every workgroup has arrived at barrier `epoch`; false when the
@@ -194,13 +196,13 @@ __device__ __forceinline__ bool grid_wait(const GridBarrier &gb, unsigned epoch)
   const unsigned nb = gridDim.x;
   __shared__ int bar_ok;
   if (threadIdx.x < GL3_WAVE) {
-    const unsigned g = threadIdx.x & 7u;
-    const unsigned gsize = nb / 8 + (g < (nb & 7u) ? 1u : 0u);
+    const unsigned g = threadIdx.x % GL3_BAR_GROUPS;
+    const unsigned gsize = nb / GL3_BAR_GROUPS + (g < (nb % GL3_BAR_GROUPS) ? 1u : 0u);
     const unsigned target = epoch * gsize;
     unsigned spins = 0;
     bool ok = true;
     for (;;) {
-      unsigned v = (threadIdx.x < 8) ? ld_coherent_u32(gb.ctr + g * GL3_BAR_STRIDE) : target;
+      unsigned v = (threadIdx.x < GL3_BAR_GROUPS) ? ld_coherent_u32(gb.ctr + g * GL3_BAR_STRIDE) : target;
       if (__all((int)(v - target) >= 0)) break;
       if (ld_coherent_u32(gb.err) != 0u || ++spins > gb.spin_limit) {
         if (threadIdx.x == 0) st_coherent_u32(gb.err, 1u);

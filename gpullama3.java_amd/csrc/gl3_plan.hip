@@ -326,9 +326,9 @@ extern "C" int gl3_create(const gl3_config *cfg, gl3_plan **out) {
   TRY(dev_alloc(p, &m.tokens_out, (size_t)cfg->context_length));
   if (cfg->flags & GL3_FLAG_PHASE_TRACE) TRY(dev_alloc(p, &m.tstamp, (size_t)(4 + 10 * L) * p->n_cu));
   unsigned *bar = nullptr;
-  TRY(dev_alloc(p, &bar, 8 * GL3_BAR_STRIDE + 64));
+  TRY(dev_alloc(p, &bar, GL3_BAR_GROUPS * GL3_BAR_STRIDE + 64));
   p->gb.ctr = bar;
-  p->gb.err = bar + 8 * GL3_BAR_STRIDE;
+  p->gb.err = bar + GL3_BAR_GROUPS * GL3_BAR_STRIDE;
   p->gb.spin_limit = 1u << 20;
   if (hipHostMalloc((void **)&p->h_state, sizeof(DecodeState)) != hipSuccess ||
       hipHostMalloc((void **)&p->h_best, sizeof(unsigned long long) * p->nbest) != hipSuccess ||
@@ -340,7 +340,7 @@ extern "C" int gl3_create(const gl3_config *cfg, gl3_plan **out) {
   if ((he = hipMemsetAsync(m.kc, 0, kv_elems * 2, p->stream)) != hipSuccess ||
       (he = hipMemsetAsync(m.vc, 0, kv_elems * 2, p->stream)) != hipSuccess ||
       (he = hipMemsetAsync(m.att_ctr, 0, (size_t)L * cfg->n_kv_heads * 4, p->stream)) != hipSuccess ||
-      (he = hipMemsetAsync(bar, 0, (8 * GL3_BAR_STRIDE + 64) * 4, p->stream)) != hipSuccess ||
+      (he = hipMemsetAsync(bar, 0, (GL3_BAR_GROUPS * GL3_BAR_STRIDE + 64) * 4, p->stream)) != hipSuccess ||
       (he = hipMemsetAsync(m.best, 0, 2 * (size_t)p->nbest * 8, p->stream)) != hipSuccess ||
       (he = hipMemsetAsync(m.x, 0, (size_t)dim * 4, p->stream)) != hipSuccess) {
     destroy_plan(p);
@@ -694,7 +694,7 @@ static int finish_timing_and_errors(gl3_plan *p) {
   p->last_kernel_ms = ksum;
   if (*p->h_err) {
     // a barrier timed out: reset the barrier counters so the plan stays usable
-    HIP_TRY(hipMemsetAsync(p->gb.ctr, 0, (8 * GL3_BAR_STRIDE + 64) * 4, p->stream));
+    HIP_TRY(hipMemsetAsync(p->gb.ctr, 0, (GL3_BAR_GROUPS * GL3_BAR_STRIDE + 64) * 4, p->stream));
     HIP_TRY(hipMemsetAsync(p->m.att_ctr, 0, (size_t)p->cfg.n_layers * p->cfg.n_kv_heads * 4, p->stream));
     HIP_TRY(hipStreamSynchronize(p->stream));
     p->epoch = 0;
