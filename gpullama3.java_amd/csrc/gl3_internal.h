@@ -26,7 +26,7 @@ hipError_t launch_finish(const ModelDev &m, hipStream_t s);
 
 bool find_step_kernel(const ModelDev &m, int grid, StepKernel *out);
 hipError_t launch_step_kernel(const StepKernel &k, const ModelDev &m, const GridBarrier &gb, unsigned epoch, int grid,
-                              hipStream_t s);
+                              int n_steps, hipStream_t s);
 
 hipError_t launch_repack_q8(const uint8_t *blocks, size_t nblocks, uint8_t *q, uint16_t *s, hipStream_t st);
 hipError_t launch_dequant_q8(const uint8_t *q, const uint16_t *s, size_t n, float *out, hipStream_t st);

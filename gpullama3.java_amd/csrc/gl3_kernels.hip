@@ -200,27 +200,30 @@ typedef Shape<FMT_Q8,  1024, 2048, 1024,  3072, 128, 2, 8, 3, Tile<1, 1, 4>, Til
 typedef Shape<FMT_F16, 3072, 3072, 3072,  8192,  96, 1, 8, 3, Tile<6, 1, 1>, Tile<6, 1, 1>, Tile<3, 2, 1>, Tile<4, 4, 2>, Tile<6, 1, 1>> ShapePhi3MiniF16;
 typedef Shape<FMT_Q8,  4096, 4096, 1024, 14336, 128, 4, 8, 3, Tile<4, 1, 2>, Tile<4, 1, 2>, Tile<4, 1, 1>, Tile<7, 2, 1>, Tile<4, 1, 2>> ShapeLlama8BQ8;
 
-// One decode step in one launch: embedding, L x (QKV, attention, Wo, gate/up,
-// down), classifier, with a grid barrier between dependent phases.  The first
+// n_steps greedy decode steps in one launch: per step embedding, L x (QKV,
+// attention, Wo, gate/up, down), classifier, with a grid barrier between
+// dependent phases and between steps.  The first
 // weight tiles of each GEMV phase are requested before the barrier that
 // precedes it (weights do not depend on it), so their HBM latency overlaps
 // the barrier.
 template <class SH>
-__global__ __launch_bounds__(GL3_STEP_BLOCK, 1) void decode_step_kernel(ModelDev m, GridBarrier gb, unsigned epoch) {
+__global__ __launch_bounds__(GL3_STEP_BLOCK, 1) void decode_step_kernel(ModelDev m, GridBarrier gb, unsigned epoch,
+                                                                        int n_steps) {
   extern __shared__ float lds[];
   __shared__ int si_lds[8];
   const int blk = blockIdx.x, nblk = gridDim.x;
   const int rows_qkv = SH::q_dim + 2 * SH::kv_dim;
+  // layer descriptors are loaded where they are used (scalar loads), so only
+  // the current phase's matrix occupies registers
+  const cLayerDev *layers = (const cLayerDev *)m.layers;
+  for (int step = 0; step < n_steps; ++step) {
   int tk = 0;
   trace(m, tk++);
   StepInfo si = read_step(m, si_lds);
   phase_embed(m, si.token, blk, nblk);
   trace(m, tk++);
   grid_arrive(gb);
-  // layer descriptors are loaded where they are used (scalar loads), so only
-  // the current phase's matrix occupies registers
-  const cLayerDev *layers = (const cLayerDev *)m.layers;
-  SH::QKV::prefetch(ld_mat(&layers[0].qkv), rows_qkv, blk, nblk);
+  if (step == 0) SH::QKV::prefetch(ld_mat(&layers[0].qkv), rows_qkv, blk, nblk);  // later steps: at the step boundary
   if (!grid_wait(gb, ++epoch)) return;
   trace(m, tk++);
   if (blk == 0) advance_step(m, si);
@@ -262,6 +265,13 @@ __global__ __launch_bounds__(GL3_STEP_BLOCK, 1) void decode_step_kernel(ModelDev
   SH::CLS::run(m.cls, m.vocab, m.x, m.out_norm, m.eps, m.logits, m.best + (size_t)si.parity * si.nbest, blk, nblk,
                lds, true);
   trace(m, tk++);
+  if (step + 1 < n_steps) {
+    // the next step reads every workgroup's argmax key and the advanced state
+    grid_arrive(gb);
+    SH::QKV::prefetch(ld_mat(&layers[0].qkv), rows_qkv, blk, nblk);
+    if (!grid_wait(gb, ++epoch)) return;
+  }
+  }
 }
 
 template <class SH>
@@ -287,7 +297,7 @@ static StepKernel make_step_kernel(const ModelDev &m, int grid) {
   StepKernel k;
   k.fn = (const void *)decode_step_kernel<SH>;
   k.lds_bytes = step_lds_bytes<SH>(m, grid);
-  k.barriers_per_step = 1 + 5 * m.n_layers;
+  k.barriers_per_step = 1 + 5 * m.n_layers;  // plus one between consecutive steps of a launch
   return k;
 }
 
@@ -301,11 +311,12 @@ bool find_step_kernel(const ModelDev &m, int grid, StepKernel *out) {
 }
 
 hipError_t launch_step_kernel(const StepKernel &k, const ModelDev &m, const GridBarrier &gb, unsigned epoch, int grid,
-                              hipStream_t s) {
+                              int n_steps, hipStream_t s) {
   ModelDev mm = m;
   GridBarrier gg = gb;
   unsigned e = epoch;
-  void *args[] = {&mm, &gg, &e};
+  int n = n_steps;
+  void *args[] = {&mm, &gg, &e, &n};
   return hipLaunchCooperativeKernel(k.fn, dim3(grid), dim3(GL3_STEP_BLOCK), args, (unsigned)k.lds_bytes, s);
 }
 

@@ -128,10 +128,16 @@ __device__ inline StepInfo read_step(const ModelDev &m, int *lds_i) {
     int from_best = __shfl(v, 2), parity = __shfl(v, 3), nbest = __shfl(v, 5);
     unsigned long long best = 0;
     if (from_best) {
+      // 4 keys per lane per 256, both 16-byte loads of a round in flight together
       const unsigned long long *src = m.best + (size_t)(parity ^ 1) * nbest;
-      for (int i = threadIdx.x; i < nbest; i += GL3_WAVE) {
-        unsigned long long k = ld_coherent_u64(src + i);
-        best = k > best ? k : best;
+      for (int i0 = 4 * threadIdx.x; i0 < nbest; i0 += 4 * GL3_WAVE) {
+        const u32x4 a = ld_coherent_x4(src, (unsigned)(i0 < nbest ? i0 : 0) * 8u);
+        const u32x4 b = ld_coherent_x4(src, (unsigned)(i0 + 2 < nbest ? i0 + 2 : 0) * 8u);
+        const unsigned long long k[4] = {((unsigned long long)a.y << 32) | a.x, ((unsigned long long)a.w << 32) | a.z,
+                                         ((unsigned long long)b.y << 32) | b.x, ((unsigned long long)b.w << 32) | b.z};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (i0 + j < nbest) best = k[j] > best ? k[j] : best;
       }
       for (int o = 32; o >= 1; o >>= 1) {
         unsigned long long other = __shfl_xor(best, o);
@@ -359,6 +365,18 @@ __device__ __forceinline__ void dma16(dma_rsrc_t r, void *lds, unsigned voff, un
   soff = __builtin_amdgcn_readfirstlane(soff);
   const unsigned m0v = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(lds_void_t *)lds);
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen nt lds"
+               :
+               : "s"(m0v), "v"(voff), "s"(r), "s"(soff)
+               : "memory", "m0");
+}
+// Same with the agent-scope sc1 bit: for the KV cache, whose rows are written
+// by whichever workgroup owns the newest position and may be read by a
+// workgroup of another XCD later in the same launch (L2 is per XCD).
+__device__ __forceinline__ void dma16_coherent(dma_rsrc_t r, void *lds, unsigned voff, unsigned soff) {
+  r = uniform(r);
+  soff = __builtin_amdgcn_readfirstlane(soff);
+  const unsigned m0v = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(lds_void_t *)lds);
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen sc1 nt lds"
                :
                : "s"(m0v), "v"(voff), "s"(r), "s"(soff)
                : "memory", "m0");
@@ -827,12 +845,12 @@ struct AttTile {
       const int ci = GL3_WAVE * i + lane, p = ci / NQ;
       int q = ci % NQ - kswz<NQ>(p);
       q = q < 0 ? q + NQ : q;
-      dma16(rk, sl + GL3_WAVE * i, (unsigned)(((t + p) * HD + 8 * q) * 2), 0u);
+      dma16_coherent(rk, sl + GL3_WAVE * i, (unsigned)(((t + p) * HD + 8 * q) * 2), 0u);
     }
 #pragma unroll
     for (int i = 0; i < NVI; ++i) {
       const int d = 32 * i + lane / 2;
-      dma16(rv, sl + KT_U4 + GL3_WAVE * i, (unsigned)((t * HD + 16 * d + 8 * (lane % 2)) * 2), 0u);
+      dma16_coherent(rv, sl + KT_U4 + GL3_WAVE * i, (unsigned)((t * HD + 16 * d + 8 * (lane % 2)) * 2), 0u);
     }
   }
 
@@ -1131,11 +1149,17 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
         vnb[i] = (unsigned)f2h(vv[2 * i]) | ((unsigned)f2h(vv[2 * i + 1]) << 16);
       }
       if (kok) {
-        // append to the cache (read by later steps)
-        *(u32x4 *)(kbase + (size_t)pos * HD + d0) = u32x4{knb[0], knb[1], knb[2], knb[3]};
+        // append to the cache with agent-scope (sc1) stores: later steps of the
+        // same launch may read these rows from another XCD
+        const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(kbase, 0, 0x7fffffff, 0x00020000);
+        const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(vbase, 0, 0x7fffffff, 0x00020000);
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{knb[0], knb[1], knb[2], knb[3]}, kr,
+                                               (unsigned)((pos * HD + d0) * 2), 0, 16 /* sc1 */);
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-          vbase[(size_t)(pos / 16) * 16 * HD + (d0 + i) * 16 + pos % 16] = (uint16_t)(vnb[i / 2] >> (16 * (i % 2)));
+          __builtin_amdgcn_raw_buffer_store_b16((unsigned short)(vnb[i / 2] >> (16 * (i % 2))), vr,
+                                                (unsigned)((((pos / 16) * HD + d0 + i) * 16 + pos % 16) * 2), 0,
+                                                16 /* sc1 */);
       }
     }
 

@@ -6,6 +6,7 @@
 // the per-phase kernels captured once in a hipGraph.
 //
 // Reference paths are relative to src/main/java/org/beehive/gpullama3/.
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -320,7 +321,7 @@ extern "C" int gl3_create(const gl3_config *cfg, gl3_plan **out) {
   TRY(dev_alloc(p, &m.part, (size_t)cfg->n_heads * m.max_split * (hd + 4)));
   TRY(dev_alloc(p, &m.att_ctr, (size_t)L * cfg->n_kv_heads));
   p->nbest = 2048;
-  if (p->n_cu > p->nbest) p->nbest = p->n_cu;
+  if (p->n_cu > p->nbest) p->nbest = (p->n_cu + 3) & ~3;  // whole 16-byte key pairs per parity half
   TRY(dev_alloc(p, &m.best, 2 * (size_t)p->nbest));
   TRY(dev_alloc(p, &m.st, 1));
   TRY(dev_alloc(p, &m.tokens_out, (size_t)cfg->context_length));
@@ -656,24 +657,30 @@ static hipEvent_t next_event(gl3_plan *p) {
   return p->ev[p->ev_used++];
 }
 
+#define GL3_STEPS_PER_LAUNCH 256
+
 static int run_steps(gl3_plan *p, int n_steps) {
   const bool timing = (p->cfg.flags & GL3_FLAG_TIMING) != 0;
   p->ev_used = 0;
   p->last_launches = 0;
   HIP_TRY(hipMemcpyAsync(p->m.st, p->h_state, sizeof(DecodeState), hipMemcpyHostToDevice, p->stream));
   HIP_TRY(hipEventRecord(p->ev_begin, p->stream));
-  for (int i = 0; i < n_steps; ++i) {
+  // persistent kernel: up to GL3_STEPS_PER_LAUNCH steps per launch (grid
+  // barriers between steps); graph schedule: one replay per step
+  for (int i = 0; i < n_steps;) {
+    const int n = p->use_step_kernel ? std::min(n_steps - i, GL3_STEPS_PER_LAUNCH) : 1;
     hipEvent_t e0 = timing ? next_event(p) : nullptr;
     if (e0) HIP_TRY(hipEventRecord(e0, p->stream));
     if (p->use_step_kernel) {
-      HIP_TRY(launch_step_kernel(p->sk, p->m, p->gb, p->epoch, p->step_grid, p->stream));
-      p->epoch += p->sk.barriers_per_step;
+      HIP_TRY(launch_step_kernel(p->sk, p->m, p->gb, p->epoch, p->step_grid, n, p->stream));
+      p->epoch += (unsigned)n * p->sk.barriers_per_step + (unsigned)(n - 1);
     } else {
       HIP_TRY(hipGraphLaunch(p->graph_exec, p->stream));
     }
     hipEvent_t e1 = timing ? next_event(p) : nullptr;
     if (e1) HIP_TRY(hipEventRecord(e1, p->stream));
     ++p->last_launches;
+    i += n;
   }
   HIP_TRY(hipEventRecord(p->ev_end, p->stream));
   return GL3_OK;
@@ -778,8 +785,9 @@ static int kv_copy(gl3_plan *p, int layer, int pos0, int npos, uint16_t *host_k,
     if (he == hipSuccess) he = hipStreamSynchronize(p->stream);  // the staging buffer is reused per head
     if (he != hipSuccess) rc = fail(GL3_ERR_DEVICE, "kv copy: %s", hipGetErrorString(he));
   }
-  hipFreeAsync(stage, p->stream);
-  hipStreamSynchronize(p->stream);
+  he = hipFreeAsync(stage, p->stream);
+  if (he == hipSuccess) he = hipStreamSynchronize(p->stream);
+  if (he != hipSuccess && rc == GL3_OK) rc = fail(GL3_ERR_DEVICE, "kv copy: %s", hipGetErrorString(he));
   return rc;
 }
 

@@ -91,6 +91,21 @@ def test_generate_greedy_matches_stepwise(gpu, sched):
     plan.free_execution_plan()
 
 
+def test_generate_greedy_across_launches(gpu):
+    """The persistent schedule decodes up to 256 tokens per launch; a run of
+    300 spans two launches and must repeat the per-token forwards exactly."""
+    shape = small("llama1b_q8", ctx=320)
+    plan, ref, _ = build(shape)
+    ref.close()
+    gen = plan.generate_greedy(3, 10, 300)
+    plan.reset()
+    tok = 3
+    for i in range(300):
+        _, tok = plan.forward(tok, 10 + i)
+        assert tok == gen[i], i
+    plan.free_execution_plan()
+
+
 def test_schedules_agree_and_are_deterministic(gpu):
     shape = small("llama1b_q8")
     a, ref, tensors = build(shape, flags=0)
