@@ -222,4 +222,69 @@ __device__ __forceinline__ bool grid_barrier(const GridBarrier &gb, unsigned epo
   return grid_wait(gb, epoch);
 }
 
+// ------------------------------------------------------------ tagged cells
+// Inside the persistent kernel, the vectors passed from one phase to the next
+// are arrays of 8-byte cells {fp32 value, 32-bit tag}.  The producer writes a
+// cell with one agent-scope 8-byte store (single-copy atomic), so a consumer
+// that reads a cell carrying the tag it expects has read that phase's value:
+// the read itself is the synchronization, with no barrier, fence or flag.  Tags
+// come from a counter that does not repeat within the life of a plan, so a
+// stale cell never carries the expected tag.  A consumer retries a cell that
+// is not ready; after spin_limit retries it raises *err, and every later wait
+// gives up at once, so a lost producer cannot hang the GPU.
+struct TagWait {
+  unsigned *err;
+  unsigned spin_limit;
+};
+
+__device__ __forceinline__ void st_tagged(uint2 *p, float v, unsigned tag) {
+  const unsigned long long w = ((unsigned long long)tag << 32) | (unsigned long long)__float_as_uint(v);
+  __hip_atomic_store((unsigned long long *)p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Slow path of a tagged read: one more poll after a short sleep; false once
+// the wait has given up.
+__device__ __forceinline__ bool tag_retry(const TagWait &tw, unsigned &spins) {
+  if (++spins > tw.spin_limit || ld_coherent_u32(tw.err) != 0u) {
+    st_coherent_u32(tw.err, 1u);
+    return false;
+  }
+  __builtin_amdgcn_s_sleep(1);
+  return true;
+}
+
+// v[n] = the 4 values of cells e[n] .. e[n] + 3 (e[n] a multiple of 4); all
+// first reads are issued before any is checked.
+template <int N>
+__device__ __forceinline__ void ld_tagged4(const uint2 *p, const int (&e)[N], unsigned tag, const TagWait &tw,
+                                           float4 (&v)[N]) {
+  u32x4 a[N], b[N];
+#pragma unroll
+  for (int n = 0; n < N; ++n) {
+    a[n] = ld_coherent_x4(p, (unsigned)e[n] * 8u);
+    b[n] = ld_coherent_x4(p, (unsigned)e[n] * 8u + 16u);
+  }
+#pragma unroll
+  for (int n = 0; n < N; ++n) {
+    unsigned spins = 0;
+    while (!(a[n].y == tag && a[n].w == tag && b[n].y == tag && b[n].w == tag)) {
+      if (!tag_retry(tw, spins)) break;
+      a[n] = ld_coherent_x4(p, (unsigned)e[n] * 8u);
+      b[n] = ld_coherent_x4(p, (unsigned)e[n] * 8u + 16u);
+    }
+    v[n] = make_float4(__uint_as_float(a[n].x), __uint_as_float(a[n].z), __uint_as_float(b[n].x),
+                       __uint_as_float(b[n].z));
+  }
+}
+
+__device__ __forceinline__ float ld_tagged1(const uint2 *p, int e, unsigned tag, const TagWait &tw) {
+  unsigned long long w = ld_coherent_u64((const unsigned long long *)(p + e));
+  unsigned spins = 0;
+  while ((unsigned)(w >> 32) != tag) {
+    if (!tag_retry(tw, spins)) break;
+    w = ld_coherent_u64((const unsigned long long *)(p + e));
+  }
+  return __uint_as_float((unsigned)w);
+}
+
 }  // namespace gl3

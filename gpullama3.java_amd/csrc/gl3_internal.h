@@ -9,7 +9,8 @@ namespace gl3 {
 struct StepKernel {
   const void *fn = nullptr;
   size_t lds_bytes = 0;
-  int barriers_per_step = 0;
+  int tags_per_step = 0;  // tagged vectors written per step
+  int max_grid = 0;       // largest grid in which every workgroup holds items of every GEMV phase
 };
 
 int gemv_n(int fmt, int K);
@@ -25,8 +26,8 @@ hipError_t launch_advance(const ModelDev &m, hipStream_t s);
 hipError_t launch_finish(const ModelDev &m, hipStream_t s);
 
 bool find_step_kernel(const ModelDev &m, int grid, StepKernel *out);
-hipError_t launch_step_kernel(const StepKernel &k, const ModelDev &m, const GridBarrier &gb, unsigned epoch, int grid,
-                              int n_steps, hipStream_t s);
+hipError_t launch_step_kernel(const StepKernel &k, const ModelDev &m, const GridBarrier &gb, unsigned epoch,
+                              unsigned tag, int grid, int n_steps, hipStream_t s);
 
 hipError_t launch_repack_q8(const uint8_t *blocks, size_t nblocks, uint8_t *q, uint16_t *s, hipStream_t st);
 hipError_t launch_dequant_q8(const uint8_t *q, const uint16_t *s, size_t n, float *out, hipStream_t st);

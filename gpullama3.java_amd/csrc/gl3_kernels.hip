@@ -3,8 +3,9 @@
 //  * per-phase kernels: embed, GEMV (store / residual / SwiGLU / logits),
 //    attention, step advance — one launch each, captured once per plan in a
 //    hipGraph and replayed per token;
-//  * decode_step_kernel<Shape>: the whole token in one cooperative launch, one
-//    workgroup per CU, phases separated by fence-free grid barriers;
+//  * decode_step_kernel<Shape>: up to 256 tokens in one cooperative launch,
+//    one workgroup per CU; phases hand their outputs on as tagged cells (each
+//    read waits for its producer), one grid barrier between tokens;
 //  * op kernels for the op-level C-ABI entry points.
 #include "gl3_internal.h"
 
@@ -30,7 +31,7 @@ template <class P>
 __global__ __launch_bounds__(GL3_BLOCK) void gemv_kernel(Mat W, int out_rows, const float *x, const float *normw,
                                                          float eps, float *y, unsigned long long *best) {
   extern __shared__ float lds[];
-  P::run(W, out_rows, x, normw, eps, y, best, blockIdx.x, gridDim.x, lds);
+  P::run(W, out_rows, InPlain{x}, normw, eps, OutPlain{y}, best, blockIdx.x, gridDim.x, lds);
 }
 
 template <class P>
@@ -86,8 +87,8 @@ __global__ __launch_bounds__(GL3_BLOCK) void logits_kernel(ModelDev m) {
   extern __shared__ float lds[];
   const int parity = ld_coherent_i32(&m.st->parity);
   const int nbest = ld_coherent_i32(&m.st->nbest);
-  P::run(m.cls, m.vocab, m.x, m.out_norm, m.eps, m.logits, m.best + (size_t)parity * nbest, blockIdx.x, gridDim.x,
-         lds);
+  P::run(m.cls, m.vocab, InPlain{m.x}, m.out_norm, m.eps, OutPlain{m.logits}, m.best + (size_t)parity * nbest,
+         blockIdx.x, gridDim.x, lds);
 }
 
 hipError_t launch_logits(const ModelDev &m, int grid, hipStream_t s) {
@@ -108,7 +109,7 @@ hipError_t launch_logits(const ModelDev &m, int grid, hipStream_t s) {
 __global__ __launch_bounds__(GL3_BLOCK) void embed_kernel(ModelDev m) {
   __shared__ int si_lds[8];
   StepInfo si = read_step(m, si_lds);
-  phase_embed(m, si.token, blockIdx.x, gridDim.x);
+  phase_embed<false>(m, si.token, blockIdx.x, gridDim.x);
 }
 
 template <int HD, int GQ>
@@ -116,7 +117,7 @@ __global__ __launch_bounds__(GL3_STEP_BLOCK) void attention_kernel(ModelDev m, i
   extern __shared__ float lds[];
   __shared__ int si_lds[8];
   StepInfo si = read_step(m, si_lds);
-  phase_attention<HD, GQ, GL3_STEP_BLOCK>(m, layer, si.pos, blockIdx.x, gridDim.x, lds);
+  phase_attention<HD, GQ, GL3_STEP_BLOCK, false>(m, layer, si.pos, blockIdx.x, gridDim.x, lds);
 }
 
 // Last kernel of a step: records the previous token and advances the control block.
@@ -201,76 +202,85 @@ typedef Shape<FMT_F16, 3072, 3072, 3072,  8192,  96, 1, 8, 3, Tile<6, 1, 1>, Til
 typedef Shape<FMT_Q8,  4096, 4096, 1024, 14336, 128, 4, 8, 3, Tile<4, 1, 2>, Tile<4, 1, 2>, Tile<4, 1, 1>, Tile<7, 2, 1>, Tile<4, 1, 2>> ShapeLlama8BQ8;
 
 // n_steps greedy decode steps in one launch: per step embedding, L x (QKV,
-// attention, Wo, gate/up, down), classifier, with a grid barrier between
-// dependent phases and between steps.  The first
-// weight tiles of each GEMV phase are requested before the barrier that
-// precedes it (weights do not depend on it), so their HBM latency overlaps
-// the barrier.
+// attention, Wo, gate/up, down), classifier.  Inside a step no phase waits at
+// a barrier: each reads its input vector as tagged cells and waits only for
+// the cells it reads (TagWait).  Every workgroup holds items of every GEMV
+// phase (the host sizes the grid so), which makes one buffer per vector (two
+// for the residual stream) safe against overwriting: a workgroup that writes
+// a vector again has waited, through the cells it read in between, for every
+// workgroup to finish reading the previous contents.  A grid barrier between
+// steps makes the argmax keys, the advanced control block and the appended
+// KV rows visible.  Each GEMV phase requests its first weight tiles before
+// it waits for its input (weights do not depend on it).
+//
+// Tags: tag0 + (1 + 5 L) s for step s's embedding, then 5 per layer (q/k/v,
+// attention, Wo output, SwiGLU, down output).
 template <class SH>
 __global__ __launch_bounds__(GL3_STEP_BLOCK, 1) void decode_step_kernel(ModelDev m, GridBarrier gb, unsigned epoch,
-                                                                        int n_steps) {
+                                                                        unsigned tag, int n_steps) {
   extern __shared__ float lds[];
   __shared__ int si_lds[8];
   const int blk = blockIdx.x, nblk = gridDim.x;
   const int rows_qkv = SH::q_dim + 2 * SH::kv_dim;
+  const TagWait tw{gb.err, gb.spin_limit};
   // layer descriptors are loaded where they are used (scalar loads), so only
   // the current phase's matrix occupies registers
   const cLayerDev *layers = (const cLayerDev *)m.layers;
   for (int step = 0; step < n_steps; ++step) {
-  int tk = 0;
-  trace(m, tk++);
-  StepInfo si = read_step(m, si_lds);
-  phase_embed(m, si.token, blk, nblk);
-  trace(m, tk++);
-  grid_arrive(gb);
-  if (step == 0) SH::QKV::prefetch(ld_mat(&layers[0].qkv), rows_qkv, blk, nblk);  // later steps: at the step boundary
-  if (!grid_wait(gb, ++epoch)) return;
-  trace(m, tk++);
-  if (blk == 0) advance_step(m, si);
-  for (int l = 0; l < m.n_layers; ++l) {
-    const cLayerDev *L = layers + l;
-    SH::QKV::run(ld_mat(&L->qkv), rows_qkv, m.x, L->attn_norm, m.eps, m.qkv, nullptr, blk, nblk, lds, true);
+    int tk = 0;
     trace(m, tk++);
-    if (!grid_barrier(gb, ++epoch)) return;
+    StepInfo si = read_step(m, si_lds);
+    unsigned t_x = tag++;  // tag of the residual stream in txa
+    phase_embed<true>(m, si.token, blk, nblk, t_x);
+    if (step == 0) SH::QKV::prefetch(ld_mat(&layers[0].qkv), rows_qkv, blk, nblk);  // later steps: at the step boundary
     trace(m, tk++);
-    // attention streams K/V through the GEMV ring: Wo's tiles are requested after it
-    phase_attention<SH::hd, SH::gqa, SH::BS>(m, l, si.pos, blk, nblk, lds);
     trace(m, tk++);
-    grid_arrive(gb);
-    SH::WO::prefetch(ld_mat(&L->wo), SH::dim, blk, nblk);
-    if (!grid_wait(gb, ++epoch)) return;
+    for (int l = 0; l < m.n_layers; ++l) {
+      const cLayerDev *L = layers + l;
+      const unsigned t_qkv = tag, t_att = tag + 1, t_wo = tag + 2, t_hb = tag + 3, t_dn = tag + 4;
+      tag += 5;
+      SH::QKV::run(ld_mat(&L->qkv), rows_qkv, InTag{m.txa, t_x, tw}, L->attn_norm, m.eps,
+                   OutTag{m.tqkv, t_qkv, nullptr, 0u, tw}, nullptr, blk, nblk, lds, true);
+      trace(m, tk++);
+      trace(m, tk++);
+      // attention streams K/V through the GEMV ring: Wo's tiles are requested after it
+      phase_attention<SH::hd, SH::gqa, SH::BS, true>(m, l, si.pos, blk, nblk, lds, t_qkv, t_att, tw);
+      trace(m, tk++);
+      SH::WO::prefetch(ld_mat(&L->wo), SH::dim, blk, nblk);
+      trace(m, tk++);
+      SH::WO::run(ld_mat(&L->wo), SH::dim, InTag{m.tatt, t_att, tw}, nullptr, m.eps, OutTag{m.txb, t_wo, m.txa, t_x, tw},
+                  nullptr, blk, nblk, lds, true);
+      trace(m, tk++);
+      SH::GU::prefetch(ld_mat(&L->gu), SH::hidden, blk, nblk);
+      trace(m, tk++);
+      SH::GU::run(ld_mat(&L->gu), SH::hidden, InTag{m.txb, t_wo, tw}, L->ffn_norm, m.eps,
+                  OutTag{m.thb, t_hb, nullptr, 0u, tw}, nullptr, blk, nblk, lds, true);
+      trace(m, tk++);
+      SH::DOWN::prefetch(ld_mat(&L->down), SH::dim, blk, nblk);
+      trace(m, tk++);
+      SH::DOWN::run(ld_mat(&L->down), SH::dim, InTag{m.thb, t_hb, tw}, nullptr, m.eps,
+                    OutTag{m.txa, t_dn, m.txb, t_wo, tw}, nullptr, blk, nblk, lds, true);
+      trace(m, tk++);
+      if (l + 1 < m.n_layers)
+        SH::QKV::prefetch(ld_mat(&layers[l + 1].qkv), rows_qkv, blk, nblk);
+      else
+        SH::CLS::prefetch(m.cls, m.vocab, blk, nblk);
+      trace(m, tk++);
+      t_x = t_dn;
+    }
+    SH::CLS::run(m.cls, m.vocab, InTag{m.txa, t_x, tw}, m.out_norm, m.eps, OutPlain{m.logits},
+                 m.best + (size_t)si.parity * si.nbest, blk, nblk, lds, true);
     trace(m, tk++);
-    SH::WO::run(ld_mat(&L->wo), SH::dim, m.att, nullptr, m.eps, m.x, nullptr, blk, nblk, lds, true);
-    trace(m, tk++);
-    grid_arrive(gb);
-    SH::GU::prefetch(ld_mat(&L->gu), SH::hidden, blk, nblk);
-    if (!grid_wait(gb, ++epoch)) return;
-    trace(m, tk++);
-    SH::GU::run(ld_mat(&L->gu), SH::hidden, m.x, L->ffn_norm, m.eps, m.hb, nullptr, blk, nblk, lds, true);
-    trace(m, tk++);
-    grid_arrive(gb);
-    SH::DOWN::prefetch(ld_mat(&L->down), SH::dim, blk, nblk);
-    if (!grid_wait(gb, ++epoch)) return;
-    trace(m, tk++);
-    SH::DOWN::run(ld_mat(&L->down), SH::dim, m.hb, nullptr, m.eps, m.x, nullptr, blk, nblk, lds, true);
-    trace(m, tk++);
-    grid_arrive(gb);
-    if (l + 1 < m.n_layers)
-      SH::QKV::prefetch(ld_mat(&layers[l + 1].qkv), rows_qkv, blk, nblk);
-    else
-      SH::CLS::prefetch(m.cls, m.vocab, blk, nblk);
-    if (!grid_wait(gb, ++epoch)) return;
-    trace(m, tk++);
-  }
-  SH::CLS::run(m.cls, m.vocab, m.x, m.out_norm, m.eps, m.logits, m.best + (size_t)si.parity * si.nbest, blk, nblk,
-               lds, true);
-  trace(m, tk++);
-  if (step + 1 < n_steps) {
-    // the next step reads every workgroup's argmax key and the advanced state
-    grid_arrive(gb);
-    SH::QKV::prefetch(ld_mat(&layers[0].qkv), rows_qkv, blk, nblk);
-    if (!grid_wait(gb, ++epoch)) return;
-  }
+    // every workgroup has read the control block: workgroup 0 waited, through
+    // the classifier input, for all down-projection rows, which every
+    // workgroup wrote after its read_step
+    if (blk == 0) advance_step(m, si);
+    if (step + 1 < n_steps) {
+      // the next step reads every workgroup's argmax key and the advanced state
+      grid_arrive(gb);
+      SH::QKV::prefetch(ld_mat(&layers[0].qkv), rows_qkv, blk, nblk);
+      if (!grid_wait(gb, ++epoch)) return;
+    }
   }
 }
 
@@ -297,7 +307,12 @@ static StepKernel make_step_kernel(const ModelDev &m, int grid) {
   StepKernel k;
   k.fn = (const void *)decode_step_kernel<SH>;
   k.lds_bytes = step_lds_bytes<SH>(m, grid);
-  k.barriers_per_step = 1 + 5 * m.n_layers;  // plus one between consecutive steps of a launch
+  k.tags_per_step = 1 + 5 * m.n_layers;  // grid barriers: one between consecutive steps of a launch
+  const int rows_qkv = SH::q_dim + 2 * SH::kv_dim;
+  const int items[5] = {SH::QKV::items(rows_qkv), SH::WO::items(SH::dim), SH::GU::items(SH::hidden),
+                        SH::DOWN::items(SH::dim), SH::CLS::items(m.vocab)};
+  k.max_grid = items[0];
+  for (int v : items) k.max_grid = v < k.max_grid ? v : k.max_grid;
   return k;
 }
 
@@ -310,13 +325,14 @@ bool find_step_kernel(const ModelDev &m, int grid, StepKernel *out) {
   return false;
 }
 
-hipError_t launch_step_kernel(const StepKernel &k, const ModelDev &m, const GridBarrier &gb, unsigned epoch, int grid,
-                              int n_steps, hipStream_t s) {
+hipError_t launch_step_kernel(const StepKernel &k, const ModelDev &m, const GridBarrier &gb, unsigned epoch,
+                              unsigned tag, int grid, int n_steps, hipStream_t s) {
+  if (grid > k.max_grid) return hipErrorInvalidValue;  // some workgroup would hold no item of a GEMV phase
   ModelDev mm = m;
   GridBarrier gg = gb;
-  unsigned e = epoch;
+  unsigned e = epoch, t = tag;
   int n = n_steps;
-  void *args[] = {&mm, &gg, &e, &n};
+  void *args[] = {&mm, &gg, &e, &t, &n};
   return hipLaunchCooperativeKernel(k.fn, dim3(grid), dim3(GL3_STEP_BLOCK), args, (unsigned)k.lds_bytes, s);
 }
 

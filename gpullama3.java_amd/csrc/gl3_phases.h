@@ -89,6 +89,10 @@ struct ModelDev {
   float *qkv;               // raw q,k,v [q_dim + 2 kv_dim]
   float *att;               // attention output [q_dim]
   float *hb;                // SwiGLU output [hidden]
+  // the same vectors as tagged cells, for the persistent kernel: residual
+  // stream ping-pong (txa: embedding and FFN outputs, txb: attention block
+  // outputs), q/k/v, attention output, SwiGLU output
+  uint2 *txa, *txb, *tqkv, *tatt, *thb;
   float *logits;            // [vocab]
   float *part;              // attention partials [n_heads][max_split][hd + 4]: o[hd], m, l, pad
   unsigned *att_ctr;        // split-merge counters [L][n_kv]
@@ -177,7 +181,8 @@ __device__ inline void advance_step(const ModelDev &m, const StepInfo &si) {
 // -------------------------------------------------------------- embedding
 // x = token_embedding_table[token] (InferenceCore.java:68; the GPU path copies
 // the fp32-converted row on the host, InferenceCore.java:586).
-__device__ inline void phase_embed(const ModelDev &m, int token, int blk, int nblk) {
+template <bool TAG>
+__device__ inline void phase_embed(const ModelDev &m, int token, int blk, int nblk, unsigned tag = 0) {
   const int dim = m.dim;
   for (int i = blk * blockDim.x + threadIdx.x; i < dim; i += nblk * blockDim.x) {
     size_t e = (size_t)token * dim + i;
@@ -189,7 +194,10 @@ __device__ inline void phase_embed(const ModelDev &m, int token, int blk, int nb
     } else {
       v = h2f(((const uint16_t *)m.embd.q)[e]);
     }
-    st_coherent(m.x + i, v);
+    if (TAG)
+      st_tagged(m.txa + i, v, tag);
+    else
+      st_coherent(m.x + i, v);
   }
 }
 
@@ -223,17 +231,65 @@ struct ChunkTraits<FMT_F16> {
 // Load x (coherently) into LDS, applying RMSNorm when normw != nullptr:
 // xs[i] = normw[i] * (ss * x[i]), ss = 1/sqrt(mean(x^2) + eps) (InferenceCore.java:46-55).
 // K must be a multiple of 4.
-template <int BS>
-__device__ inline void load_x_lds(const float *x, const float *normw, float eps, int K, float *xs, float *red) {
+// Input / output access of a phase.  Plain fp32 arrays serve the per-phase
+// kernels and the single-op entry points (ordered by kernel boundaries);
+// tagged cells serve the persistent kernel, where each read waits for its
+// producer (see TagWait).
+struct InPlain {
+  const float *p;
+  template <int N>
+  __device__ __forceinline__ void load4(const int (&e)[N], float4 (&v)[N]) const {
+#pragma unroll
+    for (int n = 0; n < N; ++n) v[n] = ld_coherent_f4(p, (unsigned)e[n]);
+  }
+};
+struct InTag {
+  const uint2 *p;
+  unsigned tag;
+  TagWait tw;
+  template <int N>
+  __device__ __forceinline__ void load4(const int (&e)[N], float4 (&v)[N]) const {
+    ld_tagged4(p, e, tag, tw, v);
+  }
+};
+// Outputs.  res_issue / res_finish read the residual input of a row in two
+// halves, so the read can be in flight during the phase.
+struct OutPlain {
+  float *y;
+  __device__ __forceinline__ unsigned long long res_issue(int row) const { return __float_as_uint(ld_coherent(y + row)); }
+  __device__ __forceinline__ float res_finish(unsigned long long r, int) const { return __uint_as_float((unsigned)r); }
+  __device__ __forceinline__ void store(int row, float v) const { st_coherent(y + row, v); }
+  __device__ __forceinline__ void store_plain(int row, float v) const { y[row] = v; }
+};
+struct OutTag {
+  uint2 *y;
+  unsigned tag;
+  const uint2 *rin;  // residual input cells (y = rin + W x)
+  unsigned rtag;
+  TagWait tw;
+  __device__ __forceinline__ unsigned long long res_issue(int row) const {
+    return ld_coherent_u64((const unsigned long long *)(rin + row));
+  }
+  __device__ __forceinline__ float res_finish(unsigned long long r, int row) const {
+    return (unsigned)(r >> 32) == rtag ? __uint_as_float((unsigned)r) : ld_tagged1(rin, row, rtag, tw);
+  }
+  __device__ __forceinline__ void store(int row, float v) const { st_tagged(y + row, v, tag); }
+  __device__ __forceinline__ void store_plain(int row, float v) const { st_tagged(y + row, v, tag); }
+};
+
+template <int BS, class IN>
+__device__ inline void load_x_lds(const IN &x, const float *normw, float eps, int K, float *xs, float *red) {
   if (!normw) {
     // batches of 4 loads per thread, all issued before the first LDS write
     for (int i0 = 4 * threadIdx.x; i0 < K; i0 += 16 * BS) {
       float4 v[4];
+      int e[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int i = i0 + u * 4 * BS;
-        v[u] = ld_coherent_f4(x, (unsigned)(i < K ? i : 0));
+        e[u] = i < K ? i : 0;
       }
+      x.load4(e, v);
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int i = i0 + u * 4 * BS;
@@ -246,7 +302,10 @@ __device__ inline void load_x_lds(const float *x, const float *normw, float eps,
   if (K > 16 * BS) {  // wide vectors: weights read after the reduction
     float ss = 0.0f;
     for (int i = 4 * threadIdx.x; i < K; i += 4 * BS) {
-      float4 v = ld_coherent_f4(x, i);
+      float4 vv[1];
+      const int e[1] = {i};
+      x.load4(e, vv);
+      const float4 v = vv[0];
       *(float4 *)(xs + i) = v;
       ss += v.x * v.x;
       ss += v.y * v.y;
@@ -266,13 +325,15 @@ __device__ inline void load_x_lds(const float *x, const float *normw, float eps,
   // sum of squares is reduced.
   float ss = 0.0f;
   float4 xv[4], wv[4];
+  int e[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int i = 4 * (threadIdx.x + u * BS);
-    const int ic = i < K ? i : 0;
-    xv[u] = ld_coherent_f4(x, (unsigned)ic);
-    wv[u] = *(const float4 *)(normw + ic);
+    e[u] = i < K ? i : 0;
   }
+  x.load4(e, xv);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) wv[u] = *(const float4 *)(normw + e[u]);
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int i = 4 * (threadIdx.x + u * BS);
@@ -615,7 +676,8 @@ struct GemvPhase {
   // MODE_LOGITS, y gets the rows and best_out[blk] the argmax key of the rows
   // this workgroup produced.  prefetched: prefetch() was already called with
   // the same W, out_rows, blk and nblk.
-  static __device__ void run(const Mat &W, int out_rows, const float *x, const float *normw, float eps, float *y,
+  template <class IN, class OUT>
+  static __device__ void run(const Mat &W, int out_rows, const IN &x, const float *normw, float eps, const OUT &y,
                              unsigned long long *best_out, int blk, int nblk, float *lds, bool prefetched = false) {
     const int K = W.cols;
     const bool stg = staged(normw != nullptr);
@@ -629,20 +691,33 @@ struct GemvPhase {
 
     const int wave = wave_id(), lane = lane_id();
     const int ks = wave % KS;
+    // residual input of the first BS local rows, read while the phase runs
+    const int nlr = nli * ROWS_PER_ITEM;
+    const int row0 = (blk + ((int)threadIdx.x / ROWS_PER_ITEM) * nblk) * ROWS_PER_ITEM + (int)threadIdx.x % ROWS_PER_ITEM;
+    unsigned long long res0 = 0;
+    if (MODE == MODE_RESIDUAL && (int)threadIdx.x < nlr && row0 < out_rows) res0 = y.res_issue(row0);
     XSlice xr;
     xr.lds = xs;
     xr.e0 = elem(K, ks, lane, 0);
     if (!stg) {
       if (XDIRECT_OK) {
+        constexpr int NV = XDIRECT_OK ? KC * EPC / 4 : 1;
+        int e[NV];
+        float4 v[NV];
+#pragma unroll
+        for (int j = 0; j < KC; ++j)
+#pragma unroll
+          for (int i = 0; i < EPC; i += 4) e[XDIRECT_OK ? j * (EPC / 4) + i / 4 : 0] = elem(K, ks, lane, j) + i;
+        x.load4(e, v);
 #pragma unroll
         for (int j = 0; j < KC; ++j)
 #pragma unroll
           for (int i = 0; i < EPC; i += 4) {
-            const float4 v = ld_coherent_f4(x, (unsigned)(elem(K, ks, lane, j) + i));
-            xr.r[j][i] = v.x;
-            xr.r[j][i + 1] = v.y;
-            xr.r[j][i + 2] = v.z;
-            xr.r[j][i + 3] = v.w;
+            const float4 w = v[XDIRECT_OK ? j * (EPC / 4) + i / 4 : 0];
+            xr.r[j][i] = w.x;
+            xr.r[j][i + 1] = w.y;
+            xr.r[j][i + 2] = w.z;
+            xr.r[j][i + 3] = w.w;
           }
       }
     } else {
@@ -677,18 +752,19 @@ struct GemvPhase {
 
     // write the rows out (coalesced over the workgroup's items)
     unsigned long long best = 0;
-    for (int lr = threadIdx.x; lr < nli * ROWS_PER_ITEM; lr += BS) {
+    for (int lr = threadIdx.x; lr < nlr; lr += BS) {
       const int row = (blk + (lr / ROWS_PER_ITEM) * nblk) * ROWS_PER_ITEM + lr % ROWS_PER_ITEM;
       if (row < out_rows) {
         const float v = obuf[lr];
         if (MODE == MODE_RESIDUAL) {
-          st_coherent(y + row, ld_coherent(y + row) + v);
+          const unsigned long long r = lr == (int)threadIdx.x ? res0 : y.res_issue(row);
+          y.store(row, y.res_finish(r, row) + v);
         } else if (MODE == MODE_LOGITS) {
-          y[row] = v;
+          y.store_plain(row, v);
           const unsigned long long k = argmax_key(v, row);
           best = k > best ? k : best;
         } else {
-          st_coherent(y + row, v);
+          y.store(row, v);
         }
       }
     }
@@ -834,12 +910,14 @@ struct AttTile {
     return ring_w<S, ATT_RING_U4>() + wave * 8 * GL3_WAVE;
   }
 
-  // DMA of this wave's u-th tile (positions t0 + 16 (wave + 4u) ..) into ring slot S
-  template <int S>
+  // DMA of this wave's u-th tile (positions t0 + 16 (wave + 4u) ..) into ring slot S.
+  // FIRST: the slot has no reads pending (the start of an item, after a
+  // workgroup barrier), so no LDS wait, which would also wait for scalar loads.
+  template <int S, bool FIRST = false>
   __device__ __forceinline__ void issue(int u) const {
     const int t = t0 + 16 * (wave + 4 * u);
     u32x4 *sl = slot<S>();
-    wait_lds();
+    if (!FIRST) wait_lds();
 #pragma unroll
     for (int i = 0; i < NKI; ++i) {
       const int ci = GL3_WAVE * i + lane, p = ci / NQ;
@@ -987,8 +1065,11 @@ struct AttTile {
   }
 };
 
-template <int HD, int GQ, int BS>
-__device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, int nblk, float *lds) {
+// q, k, v come from m.qkv (plain) or from the tagged cells m.tqkv (TAG, cells
+// written with tag_in); the output goes to m.att or, with tag_out, to m.tatt.
+template <int HD, int GQ, int BS, bool TAG>
+__device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, int nblk, float *lds,
+                                unsigned tag_in = 0, unsigned tag_out = 0, TagWait tw = TagWait{nullptr, 0}) {
   constexpr int WPB = BS / GL3_WAVE;
   constexpr int NQ = HD / 8;           // 16-byte chunks of a K row
   constexpr int NC = HD / 32;          // 32-dim chunks (score MFMAs per tile and hi/lo)
@@ -1027,9 +1108,9 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
     at.pos = pos;
     at.wave = wave;
     at.lane = lane;
-    if (ntw > 0) at.template issue<0>(0);
-    if (ntw > 1) at.template issue<1>(1);
-    if (ntw > 2) at.template issue<2>(2);
+    if (ntw > 0) at.template issue<0, true>(0);
+    if (ntw > 1) at.template issue<1, true>(1);
+    if (ntw > 2) at.template issue<2, true>(2);
 
     // ---- q of head hh (columns >= GQ stay zero), the new k and v: one round trip
     float qv[NC][8];
@@ -1039,11 +1120,24 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
       // lanes of columns >= GQ load head 0 and keep zeros (no divergent writes:
       // the arrays stay in registers)
       const bool qok = hh < GQ;
-      const float *src = m.qkv + (size_t)(kvh * GQ + (qok ? hh : 0)) * hd;
+      const int qe = (kvh * GQ + (qok ? hh : 0)) * hd;
+      float4 qa[2 * NC];
+      {
+        int e[2 * NC];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          e[2 * c] = qe + 32 * c + 8 * kb;
+          e[2 * c + 1] = qe + 32 * c + 8 * kb + 4;
+        }
+        if (TAG)
+          ld_tagged4(m.tqkv, e, tag_in, tw, qa);
+        else
+          InPlain{m.qkv}.load4(e, qa);
+      }
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const int d0 = 32 * c + 8 * kb;
-        const float4 a0 = ld_coherent_f4(src, (unsigned)d0), a1 = ld_coherent_f4(src, (unsigned)d0 + 4);
+        const float4 a0 = qa[2 * c], a1 = qa[2 * c + 1];
         float4 w0 = make_float4(1.0f, 1.0f, 1.0f, 1.0f), w1 = w0;
         if (qwen) {
           w0 = *(const float4 *)(L.q_norm + d0);
@@ -1117,11 +1211,17 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
       const bool kok = lane < NQ;
       const int d0 = 8 * (kok ? lane : 0);
       {
-        const unsigned ko = (unsigned)(m.q_dim + kvh * hd + d0), vo = ko + (unsigned)m.kv_dim;
-        f4_to(&kv[0], ld_coherent_f4(m.qkv, ko));
-        f4_to(&kv[4], ld_coherent_f4(m.qkv, ko + 4));
-        f4_to(&vv[0], ld_coherent_f4(m.qkv, vo));
-        f4_to(&vv[4], ld_coherent_f4(m.qkv, vo + 4));
+        const int ko = m.q_dim + kvh * hd + d0, vo = ko + m.kv_dim;
+        const int e[4] = {ko, ko + 4, vo, vo + 4};
+        float4 kva[4];
+        if (TAG)
+          ld_tagged4(m.tqkv, e, tag_in, tw, kva);
+        else
+          InPlain{m.qkv}.load4(e, kva);
+        f4_to(&kv[0], kva[0]);
+        f4_to(&kv[4], kva[1]);
+        f4_to(&vv[0], kva[2]);
+        f4_to(&vv[4], kva[3]);
         float4 w0 = make_float4(1.0f, 1.0f, 1.0f, 1.0f), w1 = w0;
         if (qwen) {
           w0 = *(const float4 *)(L.k_norm + d0);
@@ -1148,19 +1248,6 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
         knb[i] = (unsigned)f2h(kv[2 * i]) | ((unsigned)f2h(kv[2 * i + 1]) << 16);
         vnb[i] = (unsigned)f2h(vv[2 * i]) | ((unsigned)f2h(vv[2 * i + 1]) << 16);
       }
-      if (kok) {
-        // append to the cache with agent-scope (sc1) stores: later steps of the
-        // same launch may read these rows from another XCD
-        const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(kbase, 0, 0x7fffffff, 0x00020000);
-        const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(vbase, 0, 0x7fffffff, 0x00020000);
-        __builtin_amdgcn_raw_buffer_store_b128(u32x4{knb[0], knb[1], knb[2], knb[3]}, kr,
-                                               (unsigned)((pos * HD + d0) * 2), 0, 16 /* sc1 */);
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-          __builtin_amdgcn_raw_buffer_store_b16((unsigned short)(vnb[i / 2] >> (16 * (i % 2))), vr,
-                                                (unsigned)((((pos / 16) * HD + d0 + i) * 16 + pos % 16) * 2), 0,
-                                                16 /* sc1 */);
-      }
     }
 
     // ---- tiles
@@ -1172,6 +1259,22 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
       at.template step<0>(u, ntw, qh, ql, knb, vnb, O, mrun, lrun);
       at.template step<1>(u + 1, ntw, qh, ql, knb, vnb, O, mrun, lrun);
       at.template step<2>(u + 2, ntw, qh, ql, knb, vnb, O, mrun, lrun);
+    }
+    if (wave == wpos && lane < NQ) {
+      // append the new row to the cache, after the tiles: the stores count in
+      // vmcnt, so issued earlier they would hold up the tile waits.  Agent-scope
+      // (sc1) stores: later steps of the same launch may read the row from
+      // another XCD.
+      const int d0 = 8 * lane;
+      const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(kbase, 0, 0x7fffffff, 0x00020000);
+      const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(vbase, 0, 0x7fffffff, 0x00020000);
+      __builtin_amdgcn_raw_buffer_store_b128(u32x4{knb[0], knb[1], knb[2], knb[3]}, kr,
+                                             (unsigned)((pos * HD + d0) * 2), 0, 16 /* sc1 */);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        __builtin_amdgcn_raw_buffer_store_b16((unsigned short)(vnb[i / 2] >> (16 * (i % 2))), vr,
+                                              (unsigned)((((pos / 16) * HD + d0 + i) * 16 + pos % 16) * 2), 0,
+                                              16 /* sc1 */);
     }
     // ---- wave partials to LDS: O rows (heads) 4*kb + v, columns (dims) 16b + hh
 #pragma unroll
@@ -1224,7 +1327,11 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
         const int idx = threadIdx.x + k * BS;
         if (idx < GQ * hd) {
           const int g = idx / hd, d = idx % hd;
-          st_coherent(m.att + (size_t)(kvh * GQ + g) * hd + d, Ofin[k] / Lfin[k]);
+          const size_t o = (size_t)(kvh * GQ + g) * hd + d;
+          if (TAG)
+            st_tagged(m.tatt + o, Ofin[k] / Lfin[k], tag_out);
+          else
+            st_coherent(m.att + o, Ofin[k] / Lfin[k]);
         }
       }
       __syncthreads();
@@ -1306,11 +1413,19 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
           M = mn;
         }
         if (q == 0) {
-          float *dst = m.att + (size_t)(kvh * GQ + gg) * hd + dd;
-          st_coherent(dst + 0, O.x / Ls);
-          st_coherent(dst + 1, O.y / Ls);
-          st_coherent(dst + 2, O.z / Ls);
-          st_coherent(dst + 3, O.w / Ls);
+          const size_t o = (size_t)(kvh * GQ + gg) * hd + dd;
+          if (TAG) {
+            st_tagged(m.tatt + o + 0, O.x / Ls, tag_out);
+            st_tagged(m.tatt + o + 1, O.y / Ls, tag_out);
+            st_tagged(m.tatt + o + 2, O.z / Ls, tag_out);
+            st_tagged(m.tatt + o + 3, O.w / Ls, tag_out);
+          } else {
+            float *dst = m.att + o;
+            st_coherent(dst + 0, O.x / Ls);
+            st_coherent(dst + 1, O.y / Ls);
+            st_coherent(dst + 2, O.z / Ls);
+            st_coherent(dst + 3, O.w / Ls);
+          }
         }
       }
     }

@@ -85,7 +85,8 @@ struct gl3_plan {
   int logits_grid = 0;
   int nbest = 0;
   GridBarrier gb{};
-  unsigned epoch = 0;
+  unsigned epoch = 0;     // grid barriers completed since the counters were last zeroed
+  unsigned tag = 1;       // next tag of the persistent kernel's tagged vectors (0 = never written)
   hipGraph_t graph = nullptr;
   hipGraphExec_t graph_exec = nullptr;
 
@@ -103,6 +104,19 @@ struct gl3_plan {
   double last_elapsed_ms = 0, last_kernel_ms = 0;
   int last_launches = 0;
 };
+
+// Tagged vectors of the persistent kernel back to "never written" (tag 0).
+static hipError_t zero_tagged(gl3_plan *p) {
+  const ModelDev &m = p->m;
+  const size_t n[5] = {(size_t)m.dim, (size_t)m.dim, (size_t)(m.q_dim + 2 * m.kv_dim), (size_t)m.q_dim,
+                       (size_t)m.hidden};
+  uint2 *b[5] = {m.txa, m.txb, m.tqkv, m.tatt, m.thb};
+  for (int i = 0; i < 5; ++i) {
+    hipError_t e = hipMemsetAsync(b[i], 0, n[i] * sizeof(uint2), p->stream);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
 
 template <class T>
 static int dev_alloc(gl3_plan *p, T **out, size_t count) {
@@ -317,6 +331,11 @@ extern "C" int gl3_create(const gl3_config *cfg, gl3_plan **out) {
   TRY(dev_alloc(p, &m.qkv, p->q_dim + 2 * p->kv_dim));
   TRY(dev_alloc(p, &m.att, p->q_dim));
   TRY(dev_alloc(p, &m.hb, H));
+  TRY(dev_alloc(p, &m.txa, dim));
+  TRY(dev_alloc(p, &m.txb, dim));
+  TRY(dev_alloc(p, &m.tqkv, p->q_dim + 2 * p->kv_dim));
+  TRY(dev_alloc(p, &m.tatt, p->q_dim));
+  TRY(dev_alloc(p, &m.thb, H));
   TRY(dev_alloc(p, &m.logits, cfg->vocab_size));
   TRY(dev_alloc(p, &m.part, (size_t)cfg->n_heads * m.max_split * (hd + 4)));
   TRY(dev_alloc(p, &m.att_ctr, (size_t)L * cfg->n_kv_heads));
@@ -343,7 +362,8 @@ extern "C" int gl3_create(const gl3_config *cfg, gl3_plan **out) {
       (he = hipMemsetAsync(m.att_ctr, 0, (size_t)L * cfg->n_kv_heads * 4, p->stream)) != hipSuccess ||
       (he = hipMemsetAsync(bar, 0, (GL3_BAR_GROUPS * GL3_BAR_STRIDE + 64) * 4, p->stream)) != hipSuccess ||
       (he = hipMemsetAsync(m.best, 0, 2 * (size_t)p->nbest * 8, p->stream)) != hipSuccess ||
-      (he = hipMemsetAsync(m.x, 0, (size_t)dim * 4, p->stream)) != hipSuccess) {
+      (he = hipMemsetAsync(m.x, 0, (size_t)dim * 4, p->stream)) != hipSuccess ||
+      (he = zero_tagged(p)) != hipSuccess) {
     destroy_plan(p);
     return fail(GL3_ERR_DEVICE, "hipMemsetAsync: %s", hipGetErrorString(he));
   }
@@ -623,7 +643,7 @@ extern "C" int gl3_prepare(gl3_plan *p) {
     }
     if (per_cu >= 1) {
       p->use_step_kernel = true;
-      p->step_grid = p->n_cu;
+      p->step_grid = std::min(p->n_cu, p->sk.max_grid);
     }
   }
   p->logits_grid = p->use_step_kernel ? p->step_grid : p->nbest;
@@ -672,8 +692,14 @@ static int run_steps(gl3_plan *p, int n_steps) {
     hipEvent_t e0 = timing ? next_event(p) : nullptr;
     if (e0) HIP_TRY(hipEventRecord(e0, p->stream));
     if (p->use_step_kernel) {
-      HIP_TRY(launch_step_kernel(p->sk, p->m, p->gb, p->epoch, p->step_grid, n, p->stream));
-      p->epoch += (unsigned)n * p->sk.barriers_per_step + (unsigned)(n - 1);
+      const unsigned ntags = (unsigned)n * (unsigned)p->sk.tags_per_step;
+      if (p->tag + ntags < p->tag) {  // the tag counter would wrap: start again from clean cells
+        HIP_TRY(zero_tagged(p));
+        p->tag = 1;
+      }
+      HIP_TRY(launch_step_kernel(p->sk, p->m, p->gb, p->epoch, p->tag, p->step_grid, n, p->stream));
+      p->epoch += (unsigned)(n - 1);
+      p->tag += ntags;
     } else {
       HIP_TRY(hipGraphLaunch(p->graph_exec, p->stream));
     }
@@ -705,7 +731,7 @@ static int finish_timing_and_errors(gl3_plan *p) {
     HIP_TRY(hipMemsetAsync(p->m.att_ctr, 0, (size_t)p->cfg.n_layers * p->cfg.n_kv_heads * 4, p->stream));
     HIP_TRY(hipStreamSynchronize(p->stream));
     p->epoch = 0;
-    return fail(GL3_ERR_DEVICE, "grid barrier timed out in the per-token kernel");
+    return fail(GL3_ERR_DEVICE, "a grid barrier or a wait for a tagged vector timed out in the per-token kernel");
   }
   return GL3_OK;
 }
