@@ -93,6 +93,7 @@ struct ModelDev {
   // stream ping-pong (txa: embedding and FFN outputs, txb: attention block
   // outputs), q/k/v, attention output, SwiGLU output
   uint2 *txa, *txb, *tqkv, *tatt, *thb;
+  uint2 *tpart;             // attention partials as tagged cells, laid out as part
   float *logits;            // [vocab]
   float *part;              // attention partials [n_heads][max_split][hd + 4]: o[hd], m, l, pad
   unsigned *att_ctr;        // split-merge counters [L][n_kv]
@@ -1077,7 +1078,9 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
   static_assert(WPB == 4 && HD % 32 == 0 && HD <= 128 && GQ <= 8, "attention tile shape");
   const int hd = HD, half = HD / 2;
   const int n = pos + 1;
-  const int S = att_split_len(n, m.max_split, 16 * WPB);
+  // tagged merge: at most one item per workgroup and 64 splits per head
+  const int msplit = TAG ? max(1, min(min(m.max_split, 64), nblk / m.n_kv)) : m.max_split;
+  const int S = att_split_len(n, msplit, 16 * WPB);
   const int nsplit = (n + S - 1) / S;
   const int items = m.n_kv * nsplit;
   const int hpart = hd + 4;
@@ -1342,25 +1345,98 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
       const int idx = threadIdx.x + k * BS;
       if (idx < GQ * hd) {
         const int g = idx / hd, d = idx % hd;
-        float *pp = m.part + ((size_t)(kvh * GQ + g) * m.max_split + sp) * hpart;
-        st_coherent(pp + d, Ofin[k]);
-        if (d == 0) {
-          st_coherent(pp + hd, Mfin[k]);
-          st_coherent(pp + hd + 1, Lfin[k]);
+        const size_t po = ((size_t)(kvh * GQ + g) * m.max_split + sp) * hpart;
+        if (TAG) {
+          uint2 *pt = m.tpart + po;
+          st_tagged(pt + d, Ofin[k], tag_out);
+          if (d == 0) {
+            st_tagged(pt + hd, Mfin[k], tag_out);
+            st_tagged(pt + hd + 1, Lfin[k], tag_out);
+          }
+        } else {
+          float *pp = m.part + po;
+          st_coherent(pp + d, Ofin[k]);
+          if (d == 0) {
+            st_coherent(pp + hd, Mfin[k]);
+            st_coherent(pp + hd + 1, Lfin[k]);
+          }
         }
       }
     }
-    vmem_drain();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      unsigned *ctr = m.att_ctr + layer * m.n_kv + kvh;
-      unsigned old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const int last = (old == (unsigned)(nsplit - 1));
-      flag[0] = last;
-      if (last) st_coherent_u32(ctr, 0u);
+    bool merge;
+    if (TAG) {
+      // Every split's workgroup merges a slice of the kv head's GQ x hd
+      // outputs: float4 groups [sp * gpw, (sp + 1) * gpw), one thread per
+      // (group, split) reading that split's (m, l) and 4 dims as tagged cells,
+      // then a log-sum-exp butterfly over the spl lanes of the group.  The
+      // splits of a head wait for one another; with at most one item per
+      // workgroup (the split count is capped so) every wait ends.
+      constexpr int G4 = GQ * HD / 4;
+      const int gpw = (G4 + nsplit - 1) / nsplit;
+      int spl = 1;
+      while (spl < nsplit) spl *= 2;  // <= 64: the lanes of a group lie in one wave
+      const int gpp = BS / spl;
+      for (int g0 = 0; g0 < gpw; g0 += gpp) {
+        const int gl = g0 + (int)threadIdx.x / spl, sl = (int)threadIdx.x % spl;
+        const int gi = sp * gpw + gl;
+        const bool act = gl < gpw && gi < G4;  // uniform over the lanes of a group
+        const int gc = act ? gi : 0;
+        const int gg = (4 * gc) / HD, dd = (4 * gc) % HD;
+        const bool real = sl < nsplit;
+        const uint2 *pt = m.tpart + ((size_t)(kvh * GQ + gg) * m.max_split + (real ? sl : 0)) * hpart;
+        u32x4 rh = ld_coherent_x4(pt, (unsigned)hd * 8u);
+        u32x4 ra = ld_coherent_x4(pt, (unsigned)dd * 8u), rb = ld_coherent_x4(pt, (unsigned)dd * 8u + 16u);
+        if (act && real) {
+          unsigned spins = 0;
+          while (!(rh.y == tag_out && rh.w == tag_out && ra.y == tag_out && ra.w == tag_out && rb.y == tag_out &&
+                   rb.w == tag_out)) {
+            if (!tag_retry(tw, spins)) break;
+            rh = ld_coherent_x4(pt, (unsigned)hd * 8u);
+            ra = ld_coherent_x4(pt, (unsigned)dd * 8u);
+            rb = ld_coherent_x4(pt, (unsigned)dd * 8u + 16u);
+          }
+        }
+        float M = real ? __uint_as_float(rh.x) : -INFINITY, Ls = real ? __uint_as_float(rh.z) : 0.0f;
+        float4 O = real ? make_float4(__uint_as_float(ra.x), __uint_as_float(ra.z), __uint_as_float(rb.x),
+                                      __uint_as_float(rb.z))
+                        : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int msk = 1; msk < spl; msk <<= 1) {
+          const float M2 = __shfl_xor(M, msk), L2 = __shfl_xor(Ls, msk);
+          const float o2x = __shfl_xor(O.x, msk), o2y = __shfl_xor(O.y, msk), o2z = __shfl_xor(O.z, msk),
+                      o2w = __shfl_xor(O.w, msk);
+          const float mn = fmaxf(M, M2);
+          const float c1 = (mn == -INFINITY) ? 0.0f : __expf(M - mn);
+          const float c2 = (mn == -INFINITY) ? 0.0f : __expf(M2 - mn);
+          Ls = Ls * c1 + L2 * c2;
+          O.x = O.x * c1 + o2x * c2;
+          O.y = O.y * c1 + o2y * c2;
+          O.z = O.z * c1 + o2z * c2;
+          O.w = O.w * c1 + o2w * c2;
+          M = mn;
+        }
+        if (act && sl == 0) {
+          uint2 *dst = m.tatt + (size_t)(kvh * GQ + gg) * hd + dd;
+          st_tagged(dst + 0, O.x / Ls, tag_out);
+          st_tagged(dst + 1, O.y / Ls, tag_out);
+          st_tagged(dst + 2, O.z / Ls, tag_out);
+          st_tagged(dst + 3, O.w / Ls, tag_out);
+        }
+      }
+      merge = false;
+    } else {
+      vmem_drain();
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        unsigned *ctr = m.att_ctr + layer * m.n_kv + kvh;
+        unsigned old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int last = (old == (unsigned)(nsplit - 1));
+        flag[0] = last;
+        if (last) st_coherent_u32(ctr, 0u);
+      }
+      __syncthreads();
+      merge = flag[0] != 0;
     }
-    __syncthreads();
-    if (flag[0]) {
+    if (merge) {
       // log-sum-exp merge of the splits: out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s.
       // NT threads per 4 output dims, each folding splits s = q, q + NT, ... with all
       // loads of a batch issued before any is used; then the NT partial states merge.
@@ -1370,17 +1446,27 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
       const int pidx = threadIdx.x / nt, q = threadIdx.x % nt;
       if (pidx < npos) {
         const int gg = (4 * pidx) / hd, dd = (4 * pidx) % hd;
-        const float *base = m.part + (size_t)(kvh * GQ + gg) * m.max_split * hpart;
+        const size_t hb0 = (size_t)(kvh * GQ + gg) * m.max_split * hpart;
         float M = -INFINITY, Ls = 0.0f;
         float4 O = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         for (int s0 = q; s0 < nsplit; s0 += 8 * nt) {
           float4 hv[8], ov[8];
+          {
+            int e[16];  // (m, l) cells then the 4 output dims of 8 splits, all loads in flight together
 #pragma unroll
-          for (int b = 0; b < 8; ++b) {  // all 16 loads in flight together
-            const int s = s0 + b * nt;
-            const int sc = s < nsplit ? s : 0;
-            hv[b] = ld_coherent_f4(base, (unsigned)(sc * hpart + hd));
-            ov[b] = ld_coherent_f4(base, (unsigned)(sc * hpart + dd));
+            for (int b = 0; b < 8; ++b) {
+              const int s = s0 + b * nt;
+              const int sc = s < nsplit ? s : 0;
+              e[b] = sc * hpart + hd;
+              e[8 + b] = sc * hpart + dd;
+            }
+            float4 v[16];
+            InPlain{m.part + hb0}.load4(e, v);
+#pragma unroll
+            for (int b = 0; b < 8; ++b) {
+              hv[b] = v[b];
+              ov[b] = v[8 + b];
+            }
           }
 #pragma unroll
           for (int b = 0; b < 8; ++b) {
@@ -1413,19 +1499,11 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
           M = mn;
         }
         if (q == 0) {
-          const size_t o = (size_t)(kvh * GQ + gg) * hd + dd;
-          if (TAG) {
-            st_tagged(m.tatt + o + 0, O.x / Ls, tag_out);
-            st_tagged(m.tatt + o + 1, O.y / Ls, tag_out);
-            st_tagged(m.tatt + o + 2, O.z / Ls, tag_out);
-            st_tagged(m.tatt + o + 3, O.w / Ls, tag_out);
-          } else {
-            float *dst = m.att + o;
-            st_coherent(dst + 0, O.x / Ls);
-            st_coherent(dst + 1, O.y / Ls);
-            st_coherent(dst + 2, O.z / Ls);
-            st_coherent(dst + 3, O.w / Ls);
-          }
+          float *dst = m.att + (size_t)(kvh * GQ + gg) * hd + dd;
+          st_coherent(dst + 0, O.x / Ls);
+          st_coherent(dst + 1, O.y / Ls);
+          st_coherent(dst + 2, O.z / Ls);
+          st_coherent(dst + 3, O.w / Ls);
         }
       }
     }

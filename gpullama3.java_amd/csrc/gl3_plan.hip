@@ -108,10 +108,10 @@ struct gl3_plan {
 // Tagged vectors of the persistent kernel back to "never written" (tag 0).
 static hipError_t zero_tagged(gl3_plan *p) {
   const ModelDev &m = p->m;
-  const size_t n[5] = {(size_t)m.dim, (size_t)m.dim, (size_t)(m.q_dim + 2 * m.kv_dim), (size_t)m.q_dim,
-                       (size_t)m.hidden};
-  uint2 *b[5] = {m.txa, m.txb, m.tqkv, m.tatt, m.thb};
-  for (int i = 0; i < 5; ++i) {
+  const size_t n[6] = {(size_t)m.dim, (size_t)m.dim, (size_t)(m.q_dim + 2 * m.kv_dim), (size_t)m.q_dim,
+                       (size_t)m.hidden, (size_t)m.n_heads * m.max_split * (m.hd + 4)};
+  uint2 *b[6] = {m.txa, m.txb, m.tqkv, m.tatt, m.thb, m.tpart};
+  for (int i = 0; i < 6; ++i) {
     hipError_t e = hipMemsetAsync(b[i], 0, n[i] * sizeof(uint2), p->stream);
     if (e != hipSuccess) return e;
   }
@@ -338,6 +338,7 @@ extern "C" int gl3_create(const gl3_config *cfg, gl3_plan **out) {
   TRY(dev_alloc(p, &m.thb, H));
   TRY(dev_alloc(p, &m.logits, cfg->vocab_size));
   TRY(dev_alloc(p, &m.part, (size_t)cfg->n_heads * m.max_split * (hd + 4)));
+  TRY(dev_alloc(p, &m.tpart, (size_t)cfg->n_heads * m.max_split * (hd + 4)));
   TRY(dev_alloc(p, &m.att_ctr, (size_t)L * cfg->n_kv_heads));
   p->nbest = 2048;
   if (p->n_cu > p->nbest) p->nbest = (p->n_cu + 3) & ~3;  // whole 16-byte key pairs per parity half
