@@ -82,7 +82,7 @@ typedef enum gl3_tensor_kind {
 
 /* Plan flags */
 #define GL3_FLAG_PHASE_KERNELS 1u  /* run one kernel per phase (captured in a hipGraph) instead of
-                                      the persistent per-token kernel */
+                                      the persistent decode kernel */
 #define GL3_FLAG_TIMING 2u         /* record HIP events around every launch (gl3_get_timing) */
 #define GL3_FLAG_PHASE_TRACE 4u    /* every workgroup of the persistent kernel stamps every phase boundary */
 
@@ -162,15 +162,17 @@ int gl3_fill_kv_normal(gl3_plan *p, uint64_t seed, int npos);
  * the number of kernel launches. */
 int gl3_get_timing(gl3_plan *p, double *elapsed_ms, double *kernel_ms, int32_t *launches);
 
-/* Phase trace of the last step of the persistent per-token kernel (needs
+/* Phase trace of the last token of the persistent decode kernel (needs
  * GL3_FLAG_PHASE_TRACE): durations in microseconds, as seen by workgroup 0, of
- * embedding, barrier, then per layer {QKV, barrier, attention, barrier, Wo,
- * barrier, gate/up, barrier, down, barrier}, then the classifier.  *n_out gets
- * the number of entries written.  No reference counterpart (the reference's
- * TornadoVM profiler times whole task graphs: llama-tornado:131-134). */
+ * embedding, 0, then per layer {QKV, 0, attention, request of the Wo weights,
+ * Wo, request of the gate/up weights, gate/up, request of the down weights,
+ * down, request of the next phase's weights}, then the classifier (each phase
+ * includes its wait for its input).  *n_out gets the number of entries written.
+ * No reference counterpart (the reference's TornadoVM profiler times whole task
+ * graphs: llama-tornado:131-134). */
 int gl3_get_phase_trace(gl3_plan *p, double *us_out, int32_t max_entries, int32_t *n_out);
 
-/* Raw phase-boundary stamps of the last persistent-kernel step for every
+/* Raw phase-boundary stamps of the last persistent-kernel token for every
  * workgroup: out[i * n_workgroups + w] = s_memrealtime (100 MHz) of workgroup
  * w at boundary i (same boundaries as gl3_get_phase_trace, with the step's
  * start at i = 0).  Needs GL3_FLAG_PHASE_TRACE.  No reference counterpart. */
