@@ -195,11 +195,11 @@ struct Shape {
 };
 
 //                  fmt     dim   q_dim kv_dim hidden hd  G SC D  QKV           WO            GU            DOWN          CLS
-typedef Shape<FMT_Q8,  2048, 2048,  512,  8192,  64, 4, 8, 3, Tile<2, 1, 3>, Tile<2, 1, 2>, Tile<2, 1, 2>, Tile<2, 4, 4>, Tile<2, 1, 4>> ShapeLlama1BQ8;
+typedef Shape<FMT_Q8,  2048, 2048,  512,  8192,  64, 4, 8, 2, Tile<2, 1, 3>, Tile<2, 1, 2>, Tile<2, 1, 2>, Tile<2, 4, 4>, Tile<2, 1, 4>> ShapeLlama1BQ8;
 typedef Shape<FMT_F16, 2048, 2048,  512,  8192,  64, 4, 8, 3, Tile<4, 1, 3>, Tile<4, 1, 2>, Tile<4, 1, 1>, Tile<4, 4, 2>, Tile<4, 1, 2>> ShapeLlama1BF16;
 typedef Shape<FMT_Q8,  1024, 2048, 1024,  3072, 128, 2, 8, 3, Tile<1, 1, 4>, Tile<1, 2, 2>, Tile<1, 1, 3>, Tile<3, 1, 1>, Tile<1, 1, 8>> ShapeQwen3_06BQ8;
 typedef Shape<FMT_F16, 3072, 3072, 3072,  8192,  96, 1, 8, 3, Tile<6, 1, 1>, Tile<6, 1, 1>, Tile<3, 2, 1>, Tile<4, 4, 2>, Tile<6, 1, 1>> ShapePhi3MiniF16;
-typedef Shape<FMT_Q8,  4096, 4096, 1024, 14336, 128, 4, 8, 3, Tile<4, 1, 2>, Tile<4, 1, 2>, Tile<4, 1, 1>, Tile<7, 2, 1>, Tile<4, 1, 2>> ShapeLlama8BQ8;
+typedef Shape<FMT_Q8,  4096, 4096, 1024, 14336, 128, 4, 8, 2, Tile<4, 1, 2>, Tile<4, 1, 2>, Tile<4, 1, 1>, Tile<7, 2, 1>, Tile<4, 1, 2>> ShapeLlama8BQ8;
 
 // n_steps greedy decode steps in one launch: per step embedding, L x (QKV,
 // attention, Wo, gate/up, down), classifier.  Inside a step no phase waits at
@@ -244,7 +244,7 @@ __global__ __launch_bounds__(GL3_STEP_BLOCK, 1) void decode_step_kernel(ModelDev
       trace(m, tk++);
       trace(m, tk++);
       // attention streams K/V through the GEMV ring: Wo's tiles are requested after it
-      phase_attention<SH::hd, SH::gqa, SH::BS, true>(m, l, si.pos, blk, nblk, lds, t_qkv, t_att, tw);
+      phase_attention<SH::hd, SH::gqa, SH::BS, true, SH::QKV::WCH>(m, l, si.pos, blk, nblk, lds, t_qkv, t_att, tw);
       trace(m, tk++);
       SH::WO::prefetch(ld_mat(&L->wo), SH::dim, blk, nblk);
       trace(m, tk++);

@@ -817,7 +817,7 @@ typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 #define ATT_DEPTH 3
-#define ATT_RING_U4 (4 * 8 * GL3_WAVE)  // ring slot of the GEMV phases (4 waves x 8 KB), in u32x4
+#define ATT_RING_U4 (4 * 8 * GL3_WAVE)  // default ring slot (4 waves x 8 KB), in u32x4
 
 __device__ __forceinline__ void rope_pair(float &v0, float &v1, float c, float s) {
   float a = v0 * c - v1 * s;
@@ -898,8 +898,11 @@ __device__ __forceinline__ float inv_rms(float ss, int hd, float eps) {
 // One wave's share of a (kv head, split) item: tile DMA and tile compute.  The
 // ring slot is a template parameter so that each slot is its own LDS object and
 // the compiler's own wait counts do not serialize the slots.
-template <int HD, int GQ>
+// RU4: ring slot size in u32x4 (the GEMV phases' slot in the persistent
+// kernel, so both use one ring); a wave's tile needs 4 hd of them.
+template <int HD, int GQ, int RU4>
 struct AttTile {
+  static_assert(RU4 >= 16 * HD, "ring slot too small for a K/V tile per wave");
   static constexpr int NQ = HD / 8, NC = HD / 32, NB = HD / 16, NKI = HD / 32, NVI = HD / 32, NI = NKI + NVI;
   static constexpr int KT_U4 = 16 * NQ;
   const ModelDev *m;
@@ -908,7 +911,7 @@ struct AttTile {
 
   template <int S>
   __device__ __forceinline__ u32x4 *slot() const {
-    return ring_w<S, ATT_RING_U4>() + wave * 8 * GL3_WAVE;
+    return ring_w<S, RU4>() + wave * (RU4 / 4);
   }
 
   // DMA of this wave's u-th tile (positions t0 + 16 (wave + 4u) ..) into ring slot S.
@@ -1068,7 +1071,7 @@ struct AttTile {
 
 // q, k, v come from m.qkv (plain) or from the tagged cells m.tqkv (TAG, cells
 // written with tag_in); the output goes to m.att or, with tag_out, to m.tatt.
-template <int HD, int GQ, int BS, bool TAG>
+template <int HD, int GQ, int BS, bool TAG, int RU4 = ATT_RING_U4>
 __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, int nblk, float *lds,
                                 unsigned tag_in = 0, unsigned tag_out = 0, TagWait tw = TagWait{nullptr, 0}) {
   constexpr int WPB = BS / GL3_WAVE;
@@ -1102,7 +1105,7 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
     uint16_t *vbase = m.vc + ((size_t)layer * m.n_kv + kvh) * HD * m.ctxp;
     const dma_rsrc_t rk = rsrc(kbase), rv = rsrc(vbase);
 
-    AttTile<HD, GQ> at;
+    AttTile<HD, GQ, RU4> at;
     at.m = &m;
     at.rk = rk;
     at.rv = rv;
