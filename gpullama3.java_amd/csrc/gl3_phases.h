@@ -816,7 +816,7 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-#define ATT_DEPTH 3
+#define ATT_DEPTH 3  // K/V ring slots per wave (2 or 3)
 #define ATT_RING_U4 (4 * 8 * GL3_WAVE)  // default ring slot (4 waves x 8 KB), in u32x4
 
 __device__ __forceinline__ void rope_pair(float &v0, float &v1, float c, float s) {
@@ -943,7 +943,7 @@ struct AttTile {
     if (u >= ntw) return;
     // slot S is complete once at most the loads of the later issued tiles are outstanding
     const int later = ntw - 1 - u;
-    if (later >= 2)
+    if (ATT_DEPTH >= 3 && later >= 2)
       wait_vmem<2 * NI>();
     else if (later == 1)
       wait_vmem<NI>();
@@ -1116,7 +1116,7 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
     at.lane = lane;
     if (ntw > 0) at.template issue<0, true>(0);
     if (ntw > 1) at.template issue<1, true>(1);
-    if (ntw > 2) at.template issue<2, true>(2);
+    if (ATT_DEPTH >= 3 && ntw > 2) at.template issue<(ATT_DEPTH >= 3 ? 2 : 1), true>(2);
 
     // ---- q of head hh (columns >= GQ stay zero), the new k and v: one round trip
     float qv[NC][8];
@@ -1264,7 +1264,7 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
     for (int u = 0; u < ntw; u += ATT_DEPTH) {
       at.template step<0>(u, ntw, qh, ql, knb, vnb, O, mrun, lrun);
       at.template step<1>(u + 1, ntw, qh, ql, knb, vnb, O, mrun, lrun);
-      at.template step<2>(u + 2, ntw, qh, ql, knb, vnb, O, mrun, lrun);
+      if (ATT_DEPTH >= 3) at.template step<(ATT_DEPTH >= 3 ? 2 : 1)>(u + 2, ntw, qh, ql, knb, vnb, O, mrun, lrun);
     }
     if (wave == wpos && lane < NQ) {
       // append the new row to the cache, after the tiles: the stores count in
