@@ -52,6 +52,9 @@ __device__ __forceinline__ unsigned long long ld_coherent_u64(const unsigned lon
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // 16-byte coherent load (buffer_load_dwordx4 with the agent-scope sc1 bit).
+// `base` builds the buffer descriptor and must be the same in every lane of
+// the wave (a per-lane base turns the load into a loop over distinct bases);
+// per-lane positions go in byte_off.
 // Unlike the atomic loads above, the compiler may batch these, so a loop of
 // them keeps many requests in flight.  Out-of-range offsets read zeros.
 __device__ __forceinline__ u32x4 ld_coherent_x4(const void *base, unsigned byte_off) {
@@ -243,9 +246,11 @@ __device__ __forceinline__ void st_tagged(uint2 *p, float v, unsigned tag) {
 }
 
 // Slow path of a tagged read: one more poll after a short sleep; false once
-// the wait has given up.
+// the wait has given up.  The shared error word is read only every 32nd
+// retry: read by every waiting thread at every retry it becomes a hot spot.
 __device__ __forceinline__ bool tag_retry(const TagWait &tw, unsigned &spins) {
-  if (++spins > tw.spin_limit || ld_coherent_u32(tw.err) != 0u) {
+  ++spins;
+  if (spins > tw.spin_limit || ((spins & 31u) == 0u && ld_coherent_u32(tw.err) != 0u)) {
     st_coherent_u32(tw.err, 1u);
     return false;
   }

@@ -11,6 +11,8 @@ struct StepKernel {
   size_t lds_bytes = 0;
   int tags_per_step = 0;  // tagged vectors written per step
   int max_grid = 0;       // largest grid in which every workgroup holds items of every GEMV phase
+  int ffn = 0;            // 1: fused FFN, needs the sliced down copy, the partials buffer and grid == req_grid
+  int req_grid = 0;       // fused FFN: the only grid it runs on (-1: not possible for this shape)
 };
 
 int gemv_n(int fmt, int K);
@@ -26,6 +28,8 @@ hipError_t launch_advance(const ModelDev &m, hipStream_t s);
 hipError_t launch_finish(const ModelDev &m, hipStream_t s);
 
 bool find_step_kernel(const ModelDev &m, int grid, StepKernel *out);
+hipError_t launch_slice_q8(const uint8_t *q, const uint16_t *s, int rows, int cols, uint8_t *q_sl, uint16_t *s_sl,
+                           hipStream_t st);
 hipError_t launch_step_kernel(const StepKernel &k, const ModelDev &m, const GridBarrier &gb, unsigned epoch,
                               unsigned tag, int grid, int n_steps, hipStream_t s);
 

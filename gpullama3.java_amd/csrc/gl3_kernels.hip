@@ -182,20 +182,25 @@ template <int KC_, int KS_, int NR_>
 struct Tile {
   static constexpr int KC = KC_, KS = KS_, NR = NR_;
 };
+// FFN 1: fused FFN (gate/up rows in contiguous runs of 32 per workgroup, each
+// multiplied by its 32-column slice of Wdown, partials reduced by row);
+// needs Q8_0, a two-slot ring, hidden = 32 x grid and dim = R x grid, R <= 8.
 template <int FMT_, int DIM, int QD, int KVD, int HID, int HD, int G, int SC, int DEPTH, class TQKV, class TWO,
-          class TGU, class TDN, class TCLS>
+          class TGU, class TDN, class TCLS, int FFN = 0>
 struct Shape {
   static constexpr int fmt = FMT_, dim = DIM, q_dim = QD, kv_dim = KVD, hidden = HID, hd = HD, gqa = G;
+  static constexpr int ffn = FFN;
   static constexpr int BS = GL3_STEP_BLOCK;
   typedef GemvPhase<FMT_, TQKV::KC, TQKV::KS, TQKV::NR, MODE_STORE, BS, SC, DEPTH> QKV;
   typedef GemvPhase<FMT_, TWO::KC, TWO::KS, TWO::NR, MODE_RESIDUAL, BS, SC, DEPTH> WO;
-  typedef GemvPhase<FMT_, TGU::KC, TGU::KS, TGU::NR, MODE_SWIGLU, BS, SC, DEPTH> GU;
+  typedef GemvPhase<FMT_, TGU::KC, TGU::KS, TGU::NR, MODE_SWIGLU, BS, SC, DEPTH, FFN> GU;
+  typedef DownSliceQ8<BS, DEPTH> DS;
   typedef GemvPhase<FMT_, TDN::KC, TDN::KS, TDN::NR, MODE_RESIDUAL, BS, SC, DEPTH> DOWN;
   typedef GemvPhase<FMT_, TCLS::KC, TCLS::KS, TCLS::NR, MODE_LOGITS, BS, SC, DEPTH> CLS;
 };
 
 //                  fmt     dim   q_dim kv_dim hidden hd  G SC D  QKV           WO            GU            DOWN          CLS
-typedef Shape<FMT_Q8,  2048, 2048,  512,  8192,  64, 4, 8, 2, Tile<2, 1, 3>, Tile<2, 1, 2>, Tile<2, 1, 2>, Tile<2, 4, 4>, Tile<2, 1, 4>> ShapeLlama1BQ8;
+typedef Shape<FMT_Q8,  2048, 2048,  512,  8192,  64, 4, 8, 2, Tile<2, 1, 3>, Tile<2, 1, 2>, Tile<2, 1, 2>, Tile<2, 4, 4>, Tile<2, 1, 4>, 1> ShapeLlama1BQ8;
 typedef Shape<FMT_F16, 2048, 2048,  512,  8192,  64, 4, 8, 3, Tile<4, 1, 3>, Tile<4, 1, 2>, Tile<4, 1, 1>, Tile<4, 4, 2>, Tile<4, 1, 2>> ShapeLlama1BF16;
 typedef Shape<FMT_Q8,  1024, 2048, 1024,  3072, 128, 2, 8, 3, Tile<1, 1, 4>, Tile<1, 2, 2>, Tile<1, 1, 3>, Tile<3, 1, 1>, Tile<1, 1, 8>> ShapeQwen3_06BQ8;
 typedef Shape<FMT_F16, 3072, 3072, 3072,  8192,  96, 1, 8, 3, Tile<6, 1, 1>, Tile<6, 1, 1>, Tile<3, 2, 1>, Tile<4, 4, 2>, Tile<6, 1, 1>> ShapePhi3MiniF16;
@@ -253,19 +258,37 @@ __global__ __launch_bounds__(GL3_STEP_BLOCK, 1) void decode_step_kernel(ModelDev
       trace(m, tk++);
       SH::GU::prefetch(ld_mat(&L->gu), SH::hidden, blk, nblk);
       trace(m, tk++);
-      SH::GU::run(ld_mat(&L->gu), SH::hidden, InTag{m.txb, t_wo, tw}, L->ffn_norm, m.eps,
-                  OutTag{m.thb, t_hb, nullptr, 0u, tw}, nullptr, blk, nblk, lds, true);
-      trace(m, tk++);
-      SH::DOWN::prefetch(ld_mat(&L->down), SH::dim, blk, nblk);
-      trace(m, tk++);
-      SH::DOWN::run(ld_mat(&L->down), SH::dim, InTag{m.thb, t_hb, tw}, nullptr, m.eps,
-                    OutTag{m.txa, t_dn, m.txb, t_wo, tw}, nullptr, blk, nblk, lds, true);
-      trace(m, tk++);
-      if (l + 1 < m.n_layers)
-        SH::QKV::prefetch(ld_mat(&layers[l + 1].qkv), rows_qkv, blk, nblk);
-      else
-        SH::CLS::prefetch(m.cls, m.vocab, blk, nblk);
-      trace(m, tk++);
+      if constexpr (SH::ffn == 1) {
+        // fused FFN: this workgroup's 32 SwiGLU rows stay in LDS and meet its
+        // 32-column slice of Wdown; t_hb tags the partial sums
+        SH::GU::run(ld_mat(&L->gu), SH::hidden, InTag{m.txb, t_wo, tw}, L->ffn_norm, m.eps, OutNone{}, nullptr, blk,
+                    nblk, lds, true);
+        trace(m, tk++);
+        SH::DS::prefetch(ld_mat(&L->down_sl), SH::dim, blk);
+        trace(m, tk++);
+        SH::DS::run(SH::dim, lds + SH::GU::obuf_offset(SH::dim, true), m.tdp + (size_t)blk * SH::dim, t_hb);
+        trace(m, tk++);
+        if (l + 1 < m.n_layers)
+          SH::QKV::prefetch(ld_mat(&layers[l + 1].qkv), rows_qkv, blk, nblk);
+        else
+          SH::CLS::prefetch(m.cls, m.vocab, blk, nblk);
+        phase_reduce<SH::BS>(m.tdp, SH::dim, m.txb, t_wo, m.txa, t_dn, t_hb, tw, blk, nblk, lds);
+        trace(m, tk++);
+      } else {
+        SH::GU::run(ld_mat(&L->gu), SH::hidden, InTag{m.txb, t_wo, tw}, L->ffn_norm, m.eps,
+                    OutTag{m.thb, t_hb, nullptr, 0u, tw}, nullptr, blk, nblk, lds, true);
+        trace(m, tk++);
+        SH::DOWN::prefetch(ld_mat(&L->down), SH::dim, blk, nblk);
+        trace(m, tk++);
+        SH::DOWN::run(ld_mat(&L->down), SH::dim, InTag{m.thb, t_hb, tw}, nullptr, m.eps,
+                      OutTag{m.txa, t_dn, m.txb, t_wo, tw}, nullptr, blk, nblk, lds, true);
+        trace(m, tk++);
+        if (l + 1 < m.n_layers)
+          SH::QKV::prefetch(ld_mat(&layers[l + 1].qkv), rows_qkv, blk, nblk);
+        else
+          SH::CLS::prefetch(m.cls, m.vocab, blk, nblk);
+        trace(m, tk++);
+      }
       t_x = t_dn;
     }
     SH::CLS::run(m.cls, m.vocab, InTag{m.txa, t_x, tw}, m.out_norm, m.eps, OutPlain{m.logits},
@@ -313,6 +336,14 @@ static StepKernel make_step_kernel(const ModelDev &m, int grid) {
                         SH::DOWN::items(SH::dim), SH::CLS::items(m.vocab)};
   k.max_grid = items[0];
   for (int v : items) k.max_grid = v < k.max_grid ? v : k.max_grid;
+  k.ffn = SH::ffn;
+  if (SH::ffn == 1) {
+    // one 32-column slice of Wdown per workgroup: the grid is fixed
+    k.req_grid = SH::hidden / 32;
+    const bool ok = SH::GU::items(SH::hidden) % k.req_grid == 0 && SH::dim % k.req_grid == 0 &&
+                    SH::dim / k.req_grid <= 8 && SH::dim % (2 * SH::DS::RPU) == 0 && SH::dim == 2 * SH::DS::RPU;
+    if (!ok || k.req_grid > k.max_grid) k.req_grid = -1;  // this shape cannot run fused
+  }
   return k;
 }
 
@@ -337,6 +368,24 @@ hipError_t launch_step_kernel(const StepKernel &k, const ModelDev &m, const Grid
 }
 
 // -------------------------------------------------------------- op kernels
+
+// Q8_0 [rows][cols] (quants, scales [rows][cols/32]) -> 32-column slices:
+// q_sl[b][r][j] = q[r][32 b + j], s_sl[b][r] = s[r][b].
+__global__ void slice_q8_kernel(const uint8_t *q, const uint16_t *s, int rows, int cols, uint8_t *q_sl,
+                                uint16_t *s_sl) {
+  const size_t nb = (size_t)cols / 32, n16 = (size_t)rows * nb * 2;  // 16-byte pieces
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (size_t)gridDim.x * blockDim.x) {
+    const size_t b = i / ((size_t)rows * 2), rem = i % ((size_t)rows * 2), r = rem / 2, h = rem % 2;
+    *(u32x4 *)(q_sl + (b * rows + r) * 32 + h * 16) = *(const u32x4 *)(q + r * (size_t)cols + b * 32 + h * 16);
+    if (h == 0) s_sl[b * rows + r] = s[r * nb + b];
+  }
+}
+hipError_t launch_slice_q8(const uint8_t *q, const uint16_t *s, int rows, int cols, uint8_t *q_sl, uint16_t *s_sl,
+                           hipStream_t st) {
+  if (cols % 32 != 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(slice_q8_kernel, dim3(2048), dim3(256), 0, st, q, s, rows, cols, q_sl, s_sl);
+  return hipGetLastError();
+}
 
 __global__ void dequant_q8_kernel(const uint8_t *q, const uint16_t *s, size_t n, float *out) {
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)

@@ -31,6 +31,8 @@ struct LayerDev {
   Mat wo;     // [dim][q_dim]
   Mat gu;     // [2 hidden][dim]: gate rows then up rows (Phi3: ffn_up as is)
   Mat down;   // [dim][hidden]
+  Mat down_sl;  // Q8_0 down in 32-column slices (fused FFN of the persistent kernel): quants
+                // [hidden/32][dim][32], scales [hidden/32][dim]
   const float *attn_norm, *ffn_norm, *q_norm, *k_norm;
 };
 
@@ -94,6 +96,7 @@ struct ModelDev {
   // outputs), q/k/v, attention output, SwiGLU output
   uint2 *txa, *txb, *tqkv, *tatt, *thb;
   uint2 *tpart;             // attention partials as tagged cells, laid out as part
+  uint2 *tdp;               // fused FFN: down-projection partials [workgroup][dim] as tagged cells
   float *logits;            // [vocab]
   float *part;              // attention partials [n_heads][max_split][hd + 4]: o[hd], m, l, pad
   unsigned *att_ctr;        // split-merge counters [L][n_kv]
@@ -277,6 +280,14 @@ struct OutTag {
   __device__ __forceinline__ void store(int row, float v) const { st_tagged(y + row, v, tag); }
   __device__ __forceinline__ void store_plain(int row, float v) const { st_tagged(y + row, v, tag); }
 };
+// No global output: the row values stay in the phase's LDS row buffer (obuf)
+// for a following phase of the same workgroup.
+struct OutNone {
+  __device__ __forceinline__ unsigned long long res_issue(int) const { return 0; }
+  __device__ __forceinline__ float res_finish(unsigned long long, int) const { return 0.0f; }
+  __device__ __forceinline__ void store(int, float) const {}
+  __device__ __forceinline__ void store_plain(int, float) const {}
+};
 
 template <int BS, class IN>
 __device__ inline void load_x_lds(const IN &x, const float *normw, float eps, int K, float *xs, float *red) {
@@ -453,7 +464,9 @@ __device__ __forceinline__ void dma4(dma_rsrc_t r, void *lds, unsigned voff, uns
                : "memory", "m0");
 }
 
-template <int FMT, int KC, int KS, int NR, int MODE, int BS, int SC_ = 0, int DEPTH = 2>
+// MAP 0: workgroup blk takes items blk, blk + nblk, ...; MAP 1: the items are
+// split into nblk contiguous runs (the host checks that nblk divides them).
+template <int FMT, int KC, int KS, int NR, int MODE, int BS, int SC_ = 0, int DEPTH = 2, int MAP = 0>
 struct GemvPhase {
   typedef ChunkTraits<FMT> T;
   static constexpr int EPC = T::EPC;
@@ -490,7 +503,12 @@ struct GemvPhase {
   // items of workgroup blk
   static __host__ __device__ __forceinline__ int local_items(int out_rows, int blk, int nblk) {
     const int n = items(out_rows);
+    if (MAP == 1) return n / nblk;
     return blk < n ? (n - 1 - blk) / nblk + 1 : 0;
+  }
+  // global index of the workgroup's i-th item
+  static __device__ __forceinline__ int item_of(int i, int out_rows, int blk, int nblk) {
+    return MAP == 1 ? blk * (items(out_rows) / nblk) + i : blk + i * nblk;
   }
 
   // Issues the loads of slot-load u (the workgroup's item u / PASSES, pass u % PASSES) into ring slot S.
@@ -499,7 +517,7 @@ struct GemvPhase {
     const int wave = wave_id(), lane = lane_id();
     const int ks = wave % KS, rg = wave / KS;
     const int K = W.cols;
-    const int item = blk + (u / PASSES) * nblk, pass = PASSES > 1 ? u % PASSES : 0;
+    const int item = item_of(u / PASSES, out_rows, blk, nblk), pass = PASSES > 1 ? u % PASSES : 0;
     const int j0 = pass * JP;
     u32x4 *rw = ring_w<S, WCH>() + wave * SC * GL3_WAVE;
     const dma_rsrc_t rq = rsrc(W.q);
@@ -666,6 +684,10 @@ struct GemvPhase {
 
   // LDS layout of a phase: [x (K floats, when staged)] [red 32] [kpart] [obuf] [best keys]
   static __host__ __device__ constexpr int kpart_floats() { return RG * NR * NP * KS; }
+  // float offset of obuf (the workgroup's row values, in local item order) in the phase's LDS
+  static __host__ __device__ __forceinline__ int obuf_offset(int K, bool has_norm) {
+    return (staged(has_norm) ? K : 0) + 32 + kpart_floats();
+  }
   static __host__ __device__ __forceinline__ bool staged(bool has_norm) { return !(XDIRECT_OK && !has_norm); }
   static __host__ __device__ __forceinline__ size_t lds_bytes(int K, int out_rows, int nblk, bool has_norm) {
     const int lr = local_items(out_rows, 0, nblk) * ROWS_PER_ITEM;
@@ -694,7 +716,8 @@ struct GemvPhase {
     const int ks = wave % KS;
     // residual input of the first BS local rows, read while the phase runs
     const int nlr = nli * ROWS_PER_ITEM;
-    const int row0 = (blk + ((int)threadIdx.x / ROWS_PER_ITEM) * nblk) * ROWS_PER_ITEM + (int)threadIdx.x % ROWS_PER_ITEM;
+    const int row0 = item_of((int)threadIdx.x / ROWS_PER_ITEM, out_rows, blk, nblk) * ROWS_PER_ITEM +
+                     (int)threadIdx.x % ROWS_PER_ITEM;
     unsigned long long res0 = 0;
     if (MODE == MODE_RESIDUAL && (int)threadIdx.x < nlr && row0 < out_rows) res0 = y.res_issue(row0);
     XSlice xr;
@@ -754,7 +777,7 @@ struct GemvPhase {
     // write the rows out (coalesced over the workgroup's items)
     unsigned long long best = 0;
     for (int lr = threadIdx.x; lr < nlr; lr += BS) {
-      const int row = (blk + (lr / ROWS_PER_ITEM) * nblk) * ROWS_PER_ITEM + lr % ROWS_PER_ITEM;
+      const int row = item_of(lr / ROWS_PER_ITEM, out_rows, blk, nblk) * ROWS_PER_ITEM + lr % ROWS_PER_ITEM;
       if (row < out_rows) {
         const float v = obuf[lr];
         if (MODE == MODE_RESIDUAL) {
@@ -787,6 +810,156 @@ struct GemvPhase {
     __syncthreads();  // LDS is reused by the next phase
   }
 };
+
+// ------------------------------------------------- fused FFN (down slices)
+// When every workgroup owns 32 consecutive SwiGLU rows (one Q8_0 block of the
+// down projection's K), it multiplies them by its 32-column slice of Wdown
+// right away: 2048-row partial sums, no SwiGLU vector exchanged between
+// workgroups.  The slice is stored contiguously ([slice][row][32] quants,
+// [slice][row] scales), streamed through the ring as 1024-row slot-loads
+// (8 KB of quants and 512 B of scales per wave).  A reduce phase then sums
+// the partials of each row in a fixed order.
+template <int BS, int DEPTH>
+struct DownSliceQ8 {
+  static constexpr int WPB = BS / GL3_WAVE;
+  static constexpr int RPU = WPB * 256;             // rows per slot-load (256 per wave)
+  static constexpr int WCH = WPB * 8 * GL3_WAVE;    // u32x4 per ring slot (same ring as the GEMV phases)
+  static constexpr int SDW = WPB * 8 * 16;          // scale dwords per ring slot
+  static constexpr int NI = 8 + 2;                  // loads per wave per slot-load
+  static_assert(WPB == 4, "four waves");
+
+  static __device__ __forceinline__ int units(int rows) { return rows / RPU; }
+
+  // slot-load u (rows [u RPU, (u + 1) RPU)) of slice `slice` into ring slot S
+  template <int S>
+  static __device__ __forceinline__ void issue(const Mat &W, int rows, int slice, int u) {
+    const int wave = wave_id(), lane = lane_id();
+    const int r0 = u * RPU + wave * 256;
+    u32x4 *rw = ring_w<S, WCH>() + wave * 8 * GL3_WAVE;
+    unsigned *rs = ring_s<S, SDW>() + wave * 8 * 16;
+    const dma_rsrc_t rq = rsrc(W.q), rsc = rsrc(W.s);
+    wait_lds();
+    const unsigned qoff = (unsigned)(((size_t)slice * rows + r0) * 32);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dma16(rq, rw + i * GL3_WAVE, 16u * lane, qoff + i * 1024u);
+    const unsigned soff = (unsigned)(((size_t)slice * rows + r0) * 2);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) dma4(rsc, rs + i * GL3_WAVE, 4u * lane, soff + i * 256u);
+  }
+
+  // Partial sums of the wave's 256 rows of the slot-load held in slot S: lane l
+  // takes half l % 2 of rows 32 c + l / 2 (hv = its 16 SwiGLU values); pv[c]
+  // gets row 32 c + l / 2 in both lanes of the pair.
+  template <int S>
+  static __device__ __forceinline__ void compute(const float (&hv)[16], float (&pv)[8]) {
+    const int wave = wave_id(), lane = lane_id();
+    const u32x4 *rw = ring_w<S, WCH>() + wave * 8 * GL3_WAVE + lane;
+    const uint16_t *rs = (const uint16_t *)(ring_s<S, SDW>() + wave * 8 * 16);
+    u32x4 w[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) w[c] = rw[c * GL3_WAVE];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const unsigned ww[4] = {w[c].x, w[c].y, w[c].z, w[c].w};
+      float a = 0.0f;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        a = fmaf(sbyte<0>(ww[d]), hv[4 * d + 0], a);
+        a = fmaf(sbyte<1>(ww[d]), hv[4 * d + 1], a);
+        a = fmaf(sbyte<2>(ww[d]), hv[4 * d + 2], a);
+        a = fmaf(sbyte<3>(ww[d]), hv[4 * d + 3], a);
+      }
+      // the two halves of the row: lanes l and l ^ 1 (low half first)
+      const float o = __shfl_xor(a, 1);
+      const float blk = (lane & 1) ? o + a : a + o;
+      pv[c] = h2f(rs[c * 32 + lane / 2]) * blk;
+    }
+  }
+
+  // The whole phase for dim = 2 RPU: slot-loads 0 and 1 were issued by prefetch.
+  static __device__ __forceinline__ void prefetch(const Mat &W, int rows, int slice) {
+    issue<0>(W, rows, slice, 0);
+    issue<1>(W, rows, slice, 1);
+  }
+  static __device__ __forceinline__ void run(int rows, const float *hb_lds, uint2 *dst, unsigned tag) {
+    const int lane = lane_id();
+    float hv[16];
+#pragma unroll
+    for (int i = 0; i < 16; i += 4) {
+      const float4 v = *(const float4 *)(hb_lds + 16 * (lane & 1) + i);
+      hv[i] = v.x;
+      hv[i + 1] = v.y;
+      hv[i + 2] = v.z;
+      hv[i + 3] = v.w;
+    }
+    static_assert(DEPTH == 2, "two ring slots");
+    const int wave = wave_id();
+    // two slot-loads (dim 2048); stores only after both, so the waits count loads alone
+    float p0[8], p1[8];
+    wait_vmem<NI>();
+    compute<0>(hv, p0);
+    wait_vmem<0>();
+    compute<1>(hv, p1);
+    if ((lane & 1) == 0) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        st_tagged(dst + wave * 256 + c * 32 + lane / 2, p0[c], tag);
+        st_tagged(dst + RPU + wave * 256 + c * 32 + lane / 2, p1[c], tag);
+      }
+    }
+  }
+};
+
+// Reduce of the down partials: workgroup v owns rows [v R, (v + 1) R) with
+// R = dim / nblk (<= 8): out[row] = res[row] + sum_w part[w][row], the sum over
+// w = 0 .. nblk-1 in a fixed order (per-lane partial sums of 8 rows, then a
+// wave tree, then the 4 waves in order).
+template <int BS>
+__device__ __forceinline__ void phase_reduce(const uint2 *part, int dim, const uint2 *res, unsigned rtag, uint2 *out,
+                                             unsigned tag, unsigned ptag, const TagWait &tw, int blk, int nblk,
+                                             float *lds) {
+  constexpr int WPB = BS / GL3_WAVE;
+  const int R = dim / nblk;
+  const int row0 = blk * R;
+  const int wave = wave_id(), lane = lane_id();
+  float acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+  for (int w = threadIdx.x; w < nblk; w += BS) {
+    // R consecutive cells of workgroup w's partials (R <= 8, row0 a multiple of R)
+    const uint2 *src = part + (size_t)w * dim + row0;
+    if (R == 8) {
+      const int e[2] = {w * dim + row0, w * dim + row0 + 4};  // uniform base, per-lane offsets
+      float4 v[2];
+      ld_tagged4(part, e, ptag, tw, v);
+      acc[0] += v[0].x;
+      acc[1] += v[0].y;
+      acc[2] += v[0].z;
+      acc[3] += v[0].w;
+      acc[4] += v[1].x;
+      acc[5] += v[1].y;
+      acc[6] += v[1].z;
+      acc[7] += v[1].w;
+    } else {
+      for (int i = 0; i < R; ++i) acc[i] += ld_tagged1(src, i, ptag, tw);
+    }
+  }
+  float *red = lds;  // [WPB][8]
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float t = wave_sum(acc[i]);
+    if (lane == 0) red[wave * 8 + i] = t;
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < R) {
+    float t = 0.0f;
+#pragma unroll
+    for (int w = 0; w < WPB; ++w) t += red[w * 8 + threadIdx.x];
+    const int row = row0 + threadIdx.x;
+    st_tagged(out + row, ld_tagged1(res, row, rtag, tw) + t, tag);
+  }
+  __syncthreads();
+}
 
 // -------------------------------------------------------------- attention
 // Flash-decode over the fp16 KV cache on the matrix cores.  Work item = (kv
@@ -1386,17 +1559,19 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
         const int gc = act ? gi : 0;
         const int gg = (4 * gc) / HD, dd = (4 * gc) % HD;
         const bool real = sl < nsplit;
-        const uint2 *pt = m.tpart + ((size_t)(kvh * GQ + gg) * m.max_split + (real ? sl : 0)) * hpart;
-        u32x4 rh = ld_coherent_x4(pt, (unsigned)hd * 8u);
-        u32x4 ra = ld_coherent_x4(pt, (unsigned)dd * 8u), rb = ld_coherent_x4(pt, (unsigned)dd * 8u + 16u);
+        // uniform base (m.tpart), per-lane cell offsets
+        const unsigned pc = (unsigned)(((kvh * GQ + gg) * m.max_split + (real ? sl : 0)) * hpart);
+        const uint2 *pt = m.tpart;
+        u32x4 rh = ld_coherent_x4(pt, (pc + (unsigned)hd) * 8u);
+        u32x4 ra = ld_coherent_x4(pt, (pc + (unsigned)dd) * 8u), rb = ld_coherent_x4(pt, (pc + (unsigned)dd) * 8u + 16u);
         if (act && real) {
           unsigned spins = 0;
           while (!(rh.y == tag_out && rh.w == tag_out && ra.y == tag_out && ra.w == tag_out && rb.y == tag_out &&
                    rb.w == tag_out)) {
             if (!tag_retry(tw, spins)) break;
-            rh = ld_coherent_x4(pt, (unsigned)hd * 8u);
-            ra = ld_coherent_x4(pt, (unsigned)dd * 8u);
-            rb = ld_coherent_x4(pt, (unsigned)dd * 8u + 16u);
+            rh = ld_coherent_x4(pt, (pc + (unsigned)hd) * 8u);
+            ra = ld_coherent_x4(pt, (pc + (unsigned)dd) * 8u);
+            rb = ld_coherent_x4(pt, (pc + (unsigned)dd) * 8u + 16u);
           }
         }
         float M = real ? __uint_as_float(rh.x) : -INFINITY, Ls = real ? __uint_as_float(rh.z) : 0.0f;
@@ -1460,11 +1635,11 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
             for (int b = 0; b < 8; ++b) {
               const int s = s0 + b * nt;
               const int sc = s < nsplit ? s : 0;
-              e[b] = sc * hpart + hd;
-              e[8 + b] = sc * hpart + dd;
+              e[b] = (int)hb0 + sc * hpart + hd;  // uniform base (m.part), per-lane offsets
+              e[8 + b] = (int)hb0 + sc * hpart + dd;
             }
             float4 v[16];
-            InPlain{m.part + hb0}.load4(e, v);
+            InPlain{m.part}.load4(e, v);
 #pragma unroll
             for (int b = 0; b < 8; ++b) {
               hv[b] = v[b];

@@ -65,6 +65,9 @@ struct gl3_plan {
 
   // device model
   std::vector<DevMat> qkv, wo, gu, down;
+  std::vector<DevMat> down_sl;  // fused FFN: Wdown in 32-column slices
+  uint2 *tdp = nullptr;         // fused FFN: down partials [grid][dim]
+  int hidden = 0;
   std::vector<float *> attn_norm, ffn_norm, q_norm, k_norm;
   DevMat embd, cls;
   bool cls_tied = true;
@@ -108,10 +111,12 @@ struct gl3_plan {
 // Tagged vectors of the persistent kernel back to "never written" (tag 0).
 static hipError_t zero_tagged(gl3_plan *p) {
   const ModelDev &m = p->m;
-  const size_t n[6] = {(size_t)m.dim, (size_t)m.dim, (size_t)(m.q_dim + 2 * m.kv_dim), (size_t)m.q_dim,
-                       (size_t)m.hidden, (size_t)m.n_heads * m.max_split * (m.hd + 4)};
-  uint2 *b[6] = {m.txa, m.txb, m.tqkv, m.tatt, m.thb, m.tpart};
-  for (int i = 0; i < 6; ++i) {
+  const size_t n[7] = {(size_t)m.dim, (size_t)m.dim, (size_t)(m.q_dim + 2 * m.kv_dim), (size_t)m.q_dim,
+                       (size_t)m.hidden, (size_t)m.n_heads * m.max_split * (m.hd + 4),
+                       (size_t)p->step_grid * m.dim};
+  uint2 *b[7] = {m.txa, m.txb, m.tqkv, m.tatt, m.thb, m.tpart, m.tdp};
+  for (int i = 0; i < 7; ++i) {
+    if (!b[i]) continue;
     hipError_t e = hipMemsetAsync(b[i], 0, n[i] * sizeof(uint2), p->stream);
     if (e != hipSuccess) return e;
   }
@@ -278,6 +283,8 @@ extern "C" int gl3_create(const gl3_config *cfg, gl3_plan **out) {
   p->wo.resize(L);
   p->gu.resize(L);
   p->down.resize(L);
+  p->down_sl.resize(L);
+  p->hidden = H;
   p->attn_norm.assign(L, nullptr);
   p->ffn_norm.assign(L, nullptr);
   p->q_norm.assign(L, nullptr);
@@ -642,9 +649,27 @@ extern "C" int gl3_prepare(gl3_plan *p) {
       HIP_TRY(hipFuncSetAttribute(p->sk.fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)p->sk.lds_bytes));
       HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, p->sk.fn, GL3_STEP_BLOCK, p->sk.lds_bytes));
     }
-    if (per_cu >= 1) {
+    if (per_cu >= 1 && p->sk.ffn == 0) {
       p->use_step_kernel = true;
       p->step_grid = std::min(p->n_cu, p->sk.max_grid);
+    } else if (per_cu >= 1 && p->sk.req_grid > 0 && p->sk.req_grid <= p->n_cu) {
+      // fused FFN: a 32-column slice copy of every Wdown and the partials buffer
+      p->use_step_kernel = true;
+      p->step_grid = p->sk.req_grid;
+      int rc;
+      if (!p->tdp && (rc = dev_alloc(p, &p->tdp, (size_t)p->step_grid * c.dim))) return rc;
+      m.tdp = p->tdp;
+      for (int l = 0; l < c.n_layers; ++l) {
+        if (!p->down_sl[l].q) {
+          if ((rc = alloc_mat(p, p->down_sl[l], FMT_Q8, c.dim, p->hidden))) return rc;
+          HIP_TRY(launch_slice_q8(p->down[l].q, p->down[l].s, c.dim, p->hidden, p->down_sl[l].q, p->down_sl[l].s,
+                                  p->stream));
+        }
+        ld[l].down_sl = p->down_sl[l].view();
+      }
+      HIP_TRY(hipMemcpyAsync(p->layers_d, ld.data(), sizeof(LayerDev) * ld.size(), hipMemcpyHostToDevice, p->stream));
+      HIP_TRY(zero_tagged(p));
+      HIP_TRY(hipStreamSynchronize(p->stream));
     }
   }
   p->logits_grid = p->use_step_kernel ? p->step_grid : p->nbest;
