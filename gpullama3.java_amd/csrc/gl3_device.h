@@ -58,7 +58,13 @@ __device__ __forceinline__ unsigned long long ld_coherent_u64(const unsigned lon
 // Unlike the atomic loads above, the compiler may batch these, so a loop of
 // them keeps many requests in flight.  Out-of-range offsets read zeros.
 __device__ __forceinline__ u32x4 ld_coherent_x4(const void *base, unsigned byte_off) {
-  __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, 0x7fffffff, 0x00020000);
+  // the base is wave-uniform by contract: read it from lane 0 so the descriptor lives in SGPRs
+  const unsigned long long b = (unsigned long long)base;
+  // (readfirstlane returns int: widen through unsigned, never by sign extension)
+  const unsigned hi = (unsigned)__builtin_amdgcn_readfirstlane((unsigned)(b >> 32));
+  const unsigned lo = (unsigned)__builtin_amdgcn_readfirstlane((unsigned)b);
+  const unsigned long long ub = ((unsigned long long)hi << 32) | (unsigned long long)lo;
+  __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void *)ub, 0, 0x7fffffff, 0x00020000);
   return __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 16 /* sc1 */);
 }
 __device__ __forceinline__ float4 ld_coherent_f4(const float *base, unsigned index) {
