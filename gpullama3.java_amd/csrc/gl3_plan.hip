@@ -653,18 +653,18 @@ extern "C" int gl3_prepare(gl3_plan *p) {
       p->use_step_kernel = true;
       p->step_grid = std::min(p->n_cu, p->sk.max_grid);
     } else if (per_cu >= 1 && p->sk.req_grid > 0 && p->sk.req_grid <= p->n_cu) {
-      // fused FFN: a 32-column slice copy of every Wdown and the partials buffer
+      // fused FFN: a 32-column slice copy of every Wdown and the partials
+      // buffer; the copies are remade on every prepare (an upload since the
+      // last one may have replaced the weights)
       p->use_step_kernel = true;
       p->step_grid = p->sk.req_grid;
       int rc;
       if (!p->tdp && (rc = dev_alloc(p, &p->tdp, (size_t)p->step_grid * c.dim))) return rc;
       m.tdp = p->tdp;
       for (int l = 0; l < c.n_layers; ++l) {
-        if (!p->down_sl[l].q) {
-          if ((rc = alloc_mat(p, p->down_sl[l], FMT_Q8, c.dim, p->hidden))) return rc;
-          HIP_TRY(launch_slice_q8(p->down[l].q, p->down[l].s, c.dim, p->hidden, p->down_sl[l].q, p->down_sl[l].s,
-                                  p->stream));
-        }
+        if (!p->down_sl[l].q && (rc = alloc_mat(p, p->down_sl[l], FMT_Q8, c.dim, p->hidden))) return rc;
+        HIP_TRY(launch_slice_q8(p->down[l].q, p->down[l].s, c.dim, p->hidden, p->down_sl[l].q, p->down_sl[l].s,
+                                p->stream));
         ld[l].down_sl = p->down_sl[l].view();
       }
       HIP_TRY(hipMemcpyAsync(p->layers_d, ld.data(), sizeof(LayerDev) * ld.size(), hipMemcpyHostToDevice, p->stream));

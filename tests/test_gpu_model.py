@@ -11,6 +11,7 @@ import pytest
 
 import oracle.oracle as orc
 from gpullama3_hip import _lib as L
+from gpullama3_hip.model import synth_model
 from harness import build, prefill_kv, small, top2_margin
 
 pytestmark = pytest.mark.gpu
@@ -104,6 +105,29 @@ def test_generate_greedy_across_launches(gpu):
         _, tok = plan.forward(tok, 10 + i)
         assert tok == gen[i], i
     plan.free_execution_plan()
+
+
+@pytest.mark.parametrize("key", ["llama1b_q8", "llama8b_q8"])
+def test_upload_after_forward_replaces_ffn_weights(gpu, key):
+    """Weights uploaded after a forward are what the next forward uses, also
+    where the persistent kernel keeps a rearranged copy of an FFN matrix (the
+    sliced Wdown of the fused FFN of the 1B Q8_0 shape)."""
+    shape = small(key)
+    plan, ref, tensors = build(shape)
+    ref.close()
+    plan.forward(5, 0)
+    other = synth_model(shape, seed=99)
+    for name in ("blk.0.ffn_gate.weight", "blk.0.ffn_up.weight", "blk.1.ffn_down.weight"):
+        tensors[name] = other[name]
+        plan.upload(name, other[name][0].ggml_type, other[name][1])
+    plan.reset()
+    ref = orc.OracleModel(shape, tensors, kv_fp16=True)
+    for p, t in enumerate([5, 99, 7]):
+        lg, am = plan.forward(t, p)
+        rl = ref.forward(t, p)
+        assert np.max(np.abs(lg - rl)) <= TOL_TIGHT * rl.std()
+    plan.free_execution_plan()
+    ref.close()
 
 
 def test_schedules_agree_and_are_deterministic(gpu):
