@@ -7,6 +7,7 @@ history up to the segment's start).  Weights are random-init from a seed (no
 checkpoints).  One JSON line on stdout; details on stderr.
 
     python bench.py [--steps 256] [--warmup 8] [--config llama1b_q8] [--schedule persistent|graph]
+                    [--starts P1,P2,...]
 """
 import argparse
 import json
@@ -47,7 +48,10 @@ def kv_bytes(shape, pos):
     return 2 * shape.n_layers * shape.kv_dim * 2 * (pos + 1)
 
 
-def segments(cfg_key, steps, ctx):
+def segments(cfg_key, steps, ctx, starts=None):
+    if starts:
+        per = max(1, steps // len(starts))
+        return [(p, per) for p in starts]
     if cfg_key == "llama8b_q8":
         per = max(1, steps // 3)
         return [(p, per) for p in (8192, 16384, 32768)]
@@ -79,7 +83,7 @@ def cpu_baseline(shape, tensors, seconds=15.0):
                       f"AVX2 8-lane dots), {dt:.1f} s"}
 
 
-def copy_calibration(n_floats=256 << 20, reps=3):
+def copy_calibration(n_floats=256 << 20, reps=3, out=None):
     """A plain elementwise copy kernel of known size (reads and writes 4 * n_floats
     bytes per dispatch), run under rocprofv3 --pmc to scale FETCH_SIZE/WRITE_SIZE."""
     import torch
@@ -89,7 +93,10 @@ def copy_calibration(n_floats=256 << 20, reps=3):
         torch.mul(a, 1.0, out=b)
     torch.cuda.synchronize()
     print(json.dumps({"copy_kernel": "torch.mul(a, 1.0, out=b) float32", "bytes_read_per_dispatch": 4 * n_floats,
-                      "bytes_written_per_dispatch": 4 * n_floats, "dispatches": reps}), flush=True)
+                      "bytes_written_per_dispatch": 4 * n_floats, "dispatches": reps}), file=out or sys.stdout,
+          flush=True)
+    del a, b
+    torch.cuda.empty_cache()
 
 
 def measured_traffic(cfg_key, tokens_per_launch):
@@ -121,13 +128,21 @@ def main():
     ap.add_argument("--config", default="llama1b_q8")
     ap.add_argument("--schedule", default="persistent", choices=["persistent", "graph"])
     ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--starts", default=None,
+                    help="comma-separated segment start positions (KV history filled to each); default: the "
+                         "configuration's spread of positions")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only the plain copy kernel used to calibrate rocprofv3 byte counters")
+    ap.add_argument("--calibrate-first", action="store_true",
+                    help="run the copy kernel in this process before the benchmark, so that one rocprofv3 --pmc "
+                         "session holds both (the byte counters' scale differs between sessions)")
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration()
         return
+    if args.calibrate_first:
+        copy_calibration(out=sys.stderr)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this decode path has no multi-GPU mode (--gpus {args.gpus} refused)",
               file=sys.stderr)
@@ -150,7 +165,11 @@ def main():
     if args.warmup > 0:
         plan.generate_greedy(1, 0, args.warmup)
 
-    segs = segments(args.config, args.steps, shape.context_length)
+    starts = [int(v) for v in args.starts.split(",")] if args.starts else None
+    segs = segments(args.config, args.steps, shape.context_length, starts)
+    if any(s < 0 or s + n > shape.context_length for s, n in segs):
+        print(f"segments {segs} do not fit the context of {shape.context_length} positions", file=sys.stderr)
+        sys.exit(2)
     total_steps = sum(n for _, n in segs)
     wall = 0.0
     kern_ms = 0.0

@@ -265,7 +265,9 @@ __device__ __forceinline__ bool tag_retry(const TagWait &tw, unsigned &spins) {
 }
 
 // v[n] = the 4 values of cells e[n] .. e[n] + 3 (e[n] a multiple of 4); all
-// first reads are issued before any is checked.
+// first reads are issued before any is checked, then missing cells are polled
+// one float4 at a time (polling all of them at once multiplies the polling
+// traffic, which competes with the weight stream: measured slower).
 template <int N>
 __device__ __forceinline__ void ld_tagged4(const uint2 *p, const int (&e)[N], unsigned tag, const TagWait &tw,
                                            float4 (&v)[N]) {

@@ -247,12 +247,13 @@ __global__ __launch_bounds__(GL3_STEP_BLOCK, 1) void decode_step_kernel(ModelDev
       SH::QKV::run(ld_mat(&L->qkv), rows_qkv, InTag{m.txa, t_x, tw}, L->attn_norm, m.eps,
                    OutTag{m.tqkv, t_qkv, nullptr, 0u, tw}, nullptr, blk, nblk, lds, true);
       trace(m, tk++);
-      trace(m, tk++);
       // attention streams K/V through the GEMV ring: Wo's tiles are requested after it
-      phase_attention<SH::hd, SH::gqa, SH::BS, true, SH::QKV::WCH>(m, l, si.pos, blk, nblk, lds, t_qkv, t_att, tw);
+      // (two stamps inside: q/k/v read, tiles done)
+      phase_attention<SH::hd, SH::gqa, SH::BS, true, SH::QKV::WCH>(m, l, si.pos, blk, nblk, lds, t_qkv, t_att, tw,
+                                                                  m.tstamp ? tk : -1);
+      tk += 2;
       trace(m, tk++);
       SH::WO::prefetch(ld_mat(&L->wo), SH::dim, blk, nblk);
-      trace(m, tk++);
       SH::WO::run(ld_mat(&L->wo), SH::dim, InTag{m.tatt, t_att, tw}, nullptr, m.eps, OutTag{m.txb, t_wo, m.txa, t_x, tw},
                   nullptr, blk, nblk, lds, true);
       trace(m, tk++);

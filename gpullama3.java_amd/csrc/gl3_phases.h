@@ -332,9 +332,10 @@ __device__ inline void load_x_lds(const IN &x, const float *normw, float eps, in
     __syncthreads();
     return;
   }
-  // x and the norm weights are fetched together (all loads issued before the
-  // first use) and wait in registers (up to 4 float4 each per thread) while the
-  // sum of squares is reduced.
+  // x and the norm weights are fetched together and wait in registers (up to 4
+  // float4 each per thread) while the sum of squares is reduced.  The weights
+  // are requested first: a tagged read of x polls until its producer has
+  // written, and loads placed after the poll would cost a second round trip.
   float ss = 0.0f;
   float4 xv[4], wv[4];
   int e[4];
@@ -343,9 +344,9 @@ __device__ inline void load_x_lds(const IN &x, const float *normw, float eps, in
     const int i = 4 * (threadIdx.x + u * BS);
     e[u] = i < K ? i : 0;
   }
-  x.load4(e, xv);
 #pragma unroll
   for (int u = 0; u < 4; ++u) wv[u] = *(const float4 *)(normw + e[u]);
+  x.load4(e, xv);
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int i = 4 * (threadIdx.x + u * BS);
@@ -922,6 +923,10 @@ __device__ __forceinline__ void phase_reduce(const uint2 *part, int dim, const u
   const int R = dim / nblk;
   const int row0 = blk * R;
   const int wave = wave_id(), lane = lane_id();
+  // residual input of the workgroup's rows, requested before the partials are
+  // polled (it was written a phase earlier and is normally ready)
+  const unsigned long long res_w =
+      (int)threadIdx.x < R ? ld_coherent_u64((const unsigned long long *)(res + row0 + threadIdx.x)) : 0ull;
   float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
@@ -956,7 +961,8 @@ __device__ __forceinline__ void phase_reduce(const uint2 *part, int dim, const u
 #pragma unroll
     for (int w = 0; w < WPB; ++w) t += red[w * 8 + threadIdx.x];
     const int row = row0 + threadIdx.x;
-    st_tagged(out + row, ld_tagged1(res, row, rtag, tw) + t, tag);
+    const float r = (unsigned)(res_w >> 32) == rtag ? __uint_as_float((unsigned)res_w) : ld_tagged1(res, row, rtag, tw);
+    st_tagged(out + row, r + t, tag);
   }
   __syncthreads();
 }
@@ -1246,7 +1252,8 @@ struct AttTile {
 // written with tag_in); the output goes to m.att or, with tag_out, to m.tatt.
 template <int HD, int GQ, int BS, bool TAG, int RU4 = ATT_RING_U4>
 __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, int nblk, float *lds,
-                                unsigned tag_in = 0, unsigned tag_out = 0, TagWait tw = TagWait{nullptr, 0}) {
+                                unsigned tag_in = 0, unsigned tag_out = 0, TagWait tw = TagWait{nullptr, 0},
+                                int tk = -1) {
   constexpr int WPB = BS / GL3_WAVE;
   constexpr int NQ = HD / 8;           // 16-byte chunks of a K row
   constexpr int NC = HD / 32;          // 32-dim chunks (score MFMAs per tile and hi/lo)
@@ -1268,6 +1275,12 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
   const int hh = lane % 16, kb = lane / 16;  // MFMA column (head) and k-block of this lane
   const bool neox = m.family != FAM_LLAMA, qwen = m.family == FAM_QWEN3;
 
+  // phase trace (tk >= 0): stamps tk when q/k/v have been read and tk + 1 when
+  // the tiles are done (a workgroup without an item stamps both on its way out)
+  if (tk >= 0 && blk >= items) {
+    trace(m, tk);
+    trace(m, tk + 1);
+  }
   for (int item = blk; item < items; item += nblk) {
     const int kvh = item / nsplit, sp = item % nsplit;
     const int t0 = sp * S, t1 = min(n, t0 + S);
@@ -1291,42 +1304,85 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
     if (ntw > 1) at.template issue<1, true>(1);
     if (ATT_DEPTH >= 3 && ntw > 2) at.template issue<(ATT_DEPTH >= 3 ? 2 : 1), true>(2);
 
-    // ---- q of head hh (columns >= GQ stay zero), the new k and v: one round trip
-    float qv[NC][8];
+    // ---- q of head hh (columns >= GQ stay zero), the new k and v: one round trip.
+    // What does not depend on the QKV phase is requested first (RoPE table
+    // entries, Qwen3 norm weights); then q and, in the wave whose tile holds
+    // pos, the new k and v are read as one batch of tagged cells.
+    const int wpos = owns_pos ? ((pos - t0) / 16) % WPB : -1;  // wave whose tile holds pos
+    const bool kvw = wave == wpos;                               // uniform over the wave
+    const bool qok = hh < GQ;
+    const bool kok = lane < NQ;
+    const int d0k = 8 * (kok ? lane : 0);  // dims of the new k / v held by this lane
+    float cs[NC][8], sn[NC][8], wv[NC][8];
+    float kcs[8], ksn[8], kw[8];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int d0 = 32 * c + 8 * kb;
+      rope_entries(m, pos, d0, half, neox, cs[c], sn[c]);
+      float4 w0 = make_float4(1.0f, 1.0f, 1.0f, 1.0f), w1 = w0;
+      if (qwen) {
+        w0 = *(const float4 *)(L.q_norm + d0);
+        w1 = *(const float4 *)(L.q_norm + d0 + 4);
+      }
+      f4_to(&wv[c][0], w0);
+      f4_to(&wv[c][4], w1);
+    }
     {
-      float wv[NC][8], cs[NC][8], sn[NC][8];
-      float ss = 0.0f;
+      rope_entries(m, pos, d0k, half, neox, kcs, ksn);
+      float4 w0 = make_float4(1.0f, 1.0f, 1.0f, 1.0f), w1 = w0;
+      if (qwen) {
+        w0 = *(const float4 *)(L.k_norm + d0k);
+        w1 = *(const float4 *)(L.k_norm + d0k + 4);
+      }
+      f4_to(&kw[0], w0);
+      f4_to(&kw[4], w1);
+    }
+    float4 qa[2 * NC], kva[4];
+    {
       // lanes of columns >= GQ load head 0 and keep zeros (no divergent writes:
       // the arrays stay in registers)
-      const bool qok = hh < GQ;
       const int qe = (kvh * GQ + (qok ? hh : 0)) * hd;
-      float4 qa[2 * NC];
-      {
-        int e[2 * NC];
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          e[2 * c] = qe + 32 * c + 8 * kb;
-          e[2 * c + 1] = qe + 32 * c + 8 * kb + 4;
-        }
-        if (TAG)
-          ld_tagged4(m.tqkv, e, tag_in, tw, qa);
-        else
-          InPlain{m.qkv}.load4(e, qa);
-      }
+      const int ko = m.q_dim + kvh * hd + d0k, vo = ko + m.kv_dim;
+      int e[2 * NC + 4];
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        const int d0 = 32 * c + 8 * kb;
-        const float4 a0 = qa[2 * c], a1 = qa[2 * c + 1];
-        float4 w0 = make_float4(1.0f, 1.0f, 1.0f, 1.0f), w1 = w0;
-        if (qwen) {
-          w0 = *(const float4 *)(L.q_norm + d0);
-          w1 = *(const float4 *)(L.q_norm + d0 + 4);
-        }
-        f4_to(&qv[c][0], a0);
-        f4_to(&qv[c][4], a1);
-        f4_to(&wv[c][0], w0);
-        f4_to(&wv[c][4], w1);
-        rope_entries(m, pos, d0, half, neox, cs[c], sn[c]);
+        e[2 * c] = qe + 32 * c + 8 * kb;
+        e[2 * c + 1] = qe + 32 * c + 8 * kb + 4;
+      }
+      e[2 * NC] = ko;
+      e[2 * NC + 1] = ko + 4;
+      e[2 * NC + 2] = vo;
+      e[2 * NC + 3] = vo + 4;
+      if (kvw) {
+        float4 all[2 * NC + 4];
+        if (TAG)
+          ld_tagged4(m.tqkv, e, tag_in, tw, all);
+        else
+          InPlain{m.qkv}.load4(e, all);
+#pragma unroll
+        for (int i = 0; i < 2 * NC; ++i) qa[i] = all[i];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kva[i] = all[2 * NC + i];
+      } else {
+        int eq[2 * NC];
+#pragma unroll
+        for (int i = 0; i < 2 * NC; ++i) eq[i] = e[i];
+        if (TAG)
+          ld_tagged4(m.tqkv, eq, tag_in, tw, qa);
+        else
+          InPlain{m.qkv}.load4(eq, qa);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kva[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      }
+    }
+    if (tk >= 0 && item == blk) trace(m, tk);
+    float qv[NC][8];
+    {
+      float ss = 0.0f;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        f4_to(&qv[c][0], qa[2 * c]);
+        f4_to(&qv[c][4], qa[2 * c + 1]);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           qv[c][i] = qok ? qv[c][i] : 0.0f;
@@ -1383,45 +1439,25 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
       }
     // new k, v (fp16 bits) of the 8 dims 8*lane.. held by lanes < NQ
     unsigned knb[4] = {0u, 0u, 0u, 0u}, vnb[4] = {0u, 0u, 0u, 0u};
-    const int wpos = owns_pos ? ((pos - t0) / 16) % WPB : -1;  // wave whose tile holds pos
-    if (wave == wpos) {
-      float kv[8], vv[8], kw[8], cs[8], sn[8], par[8];
+    if (kvw) {
+      float kv[8], vv[8], par[8];
       float ss = 0.0f;
-      const bool kok = lane < NQ;
-      const int d0 = 8 * (kok ? lane : 0);
-      {
-        const int ko = m.q_dim + kvh * hd + d0, vo = ko + m.kv_dim;
-        const int e[4] = {ko, ko + 4, vo, vo + 4};
-        float4 kva[4];
-        if (TAG)
-          ld_tagged4(m.tqkv, e, tag_in, tw, kva);
-        else
-          InPlain{m.qkv}.load4(e, kva);
-        f4_to(&kv[0], kva[0]);
-        f4_to(&kv[4], kva[1]);
-        f4_to(&vv[0], kva[2]);
-        f4_to(&vv[4], kva[3]);
-        float4 w0 = make_float4(1.0f, 1.0f, 1.0f, 1.0f), w1 = w0;
-        if (qwen) {
-          w0 = *(const float4 *)(L.k_norm + d0);
-          w1 = *(const float4 *)(L.k_norm + d0 + 4);
-        }
-        f4_to(&kw[0], w0);
-        f4_to(&kw[4], w1);
-        rope_entries(m, pos, d0, half, neox, cs, sn);
+      f4_to(&kv[0], kva[0]);
+      f4_to(&kv[4], kva[1]);
+      f4_to(&vv[0], kva[2]);
+      f4_to(&vv[4], kva[3]);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) ss += kok ? kv[i] * kv[i] : 0.0f;
-      }
+      for (int i = 0; i < 8; ++i) ss += kok ? kv[i] * kv[i] : 0.0f;
       if (qwen) {
         const float si = inv_rms(row16_sum(ss), hd, m.eps);
 #pragma unroll
         for (int i = 0; i < 8; ++i) kv[i] = kw[i] * (si * kv[i]);
       }
       // NeoX partner dims d +- hd/2 live in lane +- hd/16
-      const int pl = d0 < half ? lane + half / 8 : lane - half / 8;
+      const int pl = d0k < half ? lane + half / 8 : lane - half / 8;
 #pragma unroll
       for (int i = 0; i < 8; ++i) par[i] = __shfl(kv[i], pl < 0 ? 0 : pl);
-      rope_apply(kv, par, cs, sn, neox, d0 < half);
+      rope_apply(kv, par, kcs, ksn, neox, d0k < half);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         knb[i] = (unsigned)f2h(kv[2 * i]) | ((unsigned)f2h(kv[2 * i + 1]) << 16);
@@ -1468,6 +1504,7 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
       mlp[(wave * GQ + hh) * 2 + 1] = lrun;
     }
     __syncthreads();
+    if (tk >= 0 && item == blk) trace(m, tk + 1);
     constexpr int PAIRS = (GQ * HD + BS - 1) / BS;  // per-thread (g, d) slots
     float Ofin[PAIRS], Mfin[PAIRS], Lfin[PAIRS];
 #pragma unroll
