@@ -289,29 +289,96 @@ struct OutNone {
   __device__ __forceinline__ void store_plain(int, float) const {}
 };
 
+// x staging reads exactly the float4 groups a thread owns: group u of thread t
+// is elements 4 (t + (u0 + u) BS).., so a thread polls only cells that hold
+// data (a padded slot would poll a cell it already read, first before its
+// producer had written, costing one more round trip).  Slots past K (only when
+// K is not a multiple of 4 BS) repeat element 0.
+template <int N, int BS, class IN>
+__device__ __forceinline__ void x_groups(const IN &x, int K, int u0, int (&e)[N], float4 (&v)[N]) {
+#pragma unroll
+  for (int u = 0; u < N; ++u) {
+    const int i = 4 * ((int)threadIdx.x + (u0 + u) * BS);
+    e[u] = i < K ? i : 0;
+  }
+  x.load4(e, v);
+}
+
+template <int N, int BS, class IN>
+__device__ __forceinline__ void x_copy_lds(const IN &x, int K, int u0, float *xs) {
+  int e[N];
+  float4 v[N];
+  x_groups<N, BS>(x, K, u0, e, v);
+#pragma unroll
+  for (int u = 0; u < N; ++u) {
+    const int i = 4 * ((int)threadIdx.x + (u0 + u) * BS);
+    if (i < K) *(float4 *)(xs + i) = v[u];
+  }
+}
+
+// x and the norm weights are fetched together and wait in registers while the
+// sum of squares is reduced.  The weights are requested first: a tagged read
+// of x polls until its producer has written, and loads placed after the poll
+// would cost a second round trip.
+template <int N, int BS, class IN>
+__device__ __forceinline__ void x_norm_lds(const IN &x, const float *normw, float eps, int K, float *xs, float *red) {
+  float ss = 0.0f;
+  float4 xv[N], wv[N];
+  int e[N];
+#pragma unroll
+  for (int u = 0; u < N; ++u) {
+    const int i = 4 * ((int)threadIdx.x + u * BS);
+    wv[u] = *(const float4 *)(normw + (i < K ? i : 0));
+  }
+  x_groups<N, BS>(x, K, 0, e, xv);
+#pragma unroll
+  for (int u = 0; u < N; ++u) {
+    const int i = 4 * ((int)threadIdx.x + u * BS);
+    if (i < K) {
+      ss += xv[u].x * xv[u].x;
+      ss += xv[u].y * xv[u].y;
+      ss += xv[u].z * xv[u].z;
+      ss += xv[u].w * xv[u].w;
+    }
+  }
+  ss = block_sum<BS>(ss, red);
+  ss /= (float)K;
+  ss += eps;
+  ss = (float)(1.0 / sqrt((double)ss));
+#pragma unroll
+  for (int u = 0; u < N; ++u) {
+    const int i = 4 * ((int)threadIdx.x + u * BS);
+    if (i < K) {
+      float4 v = xv[u];
+      v.x = wv[u].x * (ss * v.x);
+      v.y = wv[u].y * (ss * v.y);
+      v.z = wv[u].z * (ss * v.z);
+      v.w = wv[u].w * (ss * v.w);
+      *(float4 *)(xs + i) = v;
+    }
+  }
+}
+
 template <int BS, class IN>
 __device__ inline void load_x_lds(const IN &x, const float *normw, float eps, int K, float *xs, float *red) {
+  const int ng = (K + 4 * BS - 1) / (4 * BS);  // float4 groups per thread
   if (!normw) {
-    // batches of 4 loads per thread, all issued before the first LDS write
-    for (int i0 = 4 * threadIdx.x; i0 < K; i0 += 16 * BS) {
-      float4 v[4];
-      int e[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int i = i0 + u * 4 * BS;
-        e[u] = i < K ? i : 0;
-      }
-      x.load4(e, v);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int i = i0 + u * 4 * BS;
-        if (i < K) *(float4 *)(xs + i) = v[u];
-      }
+    // batches of up to 4 groups per thread, all loads of a batch issued before the first LDS write
+    for (int u0 = 0; u0 < ng; u0 += 4) {
+      const int r = ng - u0;
+      if (r >= 4)
+        x_copy_lds<4, BS>(x, K, u0, xs);
+      else if (r == 3)
+        x_copy_lds<3, BS>(x, K, u0, xs);
+      else if (r == 2)
+        x_copy_lds<2, BS>(x, K, u0, xs);
+      else
+        x_copy_lds<1, BS>(x, K, u0, xs);
     }
     __syncthreads();
     return;
   }
-  if (K > 16 * BS) {  // wide vectors: weights read after the reduction
+  if (ng > 4) {  // wide vectors: weights read after the reduction
     float ss = 0.0f;
     for (int i = 4 * threadIdx.x; i < K; i += 4 * BS) {
       float4 vv[1];
@@ -332,47 +399,14 @@ __device__ inline void load_x_lds(const IN &x, const float *normw, float eps, in
     __syncthreads();
     return;
   }
-  // x and the norm weights are fetched together and wait in registers (up to 4
-  // float4 each per thread) while the sum of squares is reduced.  The weights
-  // are requested first: a tagged read of x polls until its producer has
-  // written, and loads placed after the poll would cost a second round trip.
-  float ss = 0.0f;
-  float4 xv[4], wv[4];
-  int e[4];
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int i = 4 * (threadIdx.x + u * BS);
-    e[u] = i < K ? i : 0;
-  }
-#pragma unroll
-  for (int u = 0; u < 4; ++u) wv[u] = *(const float4 *)(normw + e[u]);
-  x.load4(e, xv);
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int i = 4 * (threadIdx.x + u * BS);
-    if (i < K) {
-      ss += xv[u].x * xv[u].x;
-      ss += xv[u].y * xv[u].y;
-      ss += xv[u].z * xv[u].z;
-      ss += xv[u].w * xv[u].w;
-    }
-  }
-  ss = block_sum<BS>(ss, red);
-  ss /= (float)K;
-  ss += eps;
-  ss = (float)(1.0 / sqrt((double)ss));
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int i = 4 * (threadIdx.x + u * BS);
-    if (i < K) {
-      float4 v = xv[u];
-      v.x = wv[u].x * (ss * v.x);
-      v.y = wv[u].y * (ss * v.y);
-      v.z = wv[u].z * (ss * v.z);
-      v.w = wv[u].w * (ss * v.w);
-      *(float4 *)(xs + i) = v;
-    }
-  }
+  if (ng == 4)
+    x_norm_lds<4, BS>(x, normw, eps, K, xs, red);
+  else if (ng == 3)
+    x_norm_lds<3, BS>(x, normw, eps, K, xs, red);
+  else if (ng == 2)
+    x_norm_lds<2, BS>(x, normw, eps, K, xs, red);
+  else
+    x_norm_lds<1, BS>(x, normw, eps, K, xs, red);
   __syncthreads();
 }
 
@@ -1012,10 +1046,11 @@ __host__ __device__ __forceinline__ int att_split_len(int n, int max_split, int 
   return s < step ? step : s;
 }
 
-// LDS floats of the attention phase: per-wave o [wpb][G][hd], (m, l) [wpb][G][2] and a flag.
+// LDS floats of the attention phase: per-wave o [wpb][G][hd], (m, l) [wpb][G][2], a flag
+// (16 floats) and the staged q [G][hd], new k [hd] and new v [hd].
 __host__ __device__ __forceinline__ int att_lds_floats(int hd, int G, int wpb, int max_split) {
   (void)max_split;
-  return wpb * G * (hd + 2) + 16;
+  return wpb * G * (hd + 2) + 16 + (G + 2) * hd;
 }
 
 __device__ __forceinline__ void f4_to(float *dst, float4 v) {
@@ -1270,6 +1305,7 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
   float *opart = lds;                     // per-wave o [WPB][GQ][hd]
   float *mlp = opart + WPB * GQ * hd;     // per-wave (m, l) [WPB][GQ][2]
   int *flag = (int *)(mlp + WPB * GQ * 2);
+  float *qst = mlp + WPB * GQ * 2 + 16;   // staged q [GQ][hd], new k [hd], new v [hd]
   const LayerDev L = ld_layer(m.layers, layer);
   const int wave = wave_id(), lane = lane_id();
   const int hh = lane % 16, kb = lane / 16;  // MFMA column (head) and k-block of this lane
@@ -1339,38 +1375,37 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
     }
     float4 qa[2 * NC], kva[4];
     {
-      // lanes of columns >= GQ load head 0 and keep zeros (no divergent writes:
-      // the arrays stay in registers)
-      const int qe = (kvh * GQ + (qok ? hh : 0)) * hd;
-      const int ko = m.q_dim + kvh * hd + d0k, vo = ko + m.kv_dim;
-      int e[2 * NC + 4];
+      // q of the kv head's GQ heads and, in the split holding pos, the new k
+      // and v are read once per workgroup, one float4 of tagged cells per
+      // thread (all reads of the workgroup in one round trip), staged in LDS
+      // and then taken by every wave: reading them per lane would poll each
+      // cell up to 16 times (4 waves x the 16 MFMA columns).
+      const int nq4 = GQ * HD / 4, nst4 = nq4 + (owns_pos ? HD / 2 : 0);
+      for (int t = threadIdx.x; t < nst4; t += BS) {
+        const int e1[1] = {t < nq4 ? kvh * GQ * HD + 4 * t
+                                   : (t < nq4 + HD / 4 ? m.q_dim + kvh * HD + 4 * (t - nq4)
+                                                       : m.q_dim + m.kv_dim + kvh * HD + 4 * (t - nq4 - HD / 4))};
+        float4 v1[1];
+        if (TAG)
+          ld_tagged4(m.tqkv, e1, tag_in, tw, v1);
+        else
+          InPlain{m.qkv}.load4(e1, v1);
+        *(float4 *)(qst + 4 * t) = v1[0];
+      }
+      __syncthreads();
+      // lanes of columns >= GQ take head 0 and keep zeros
+      const float *qh0 = qst + (qok ? hh : 0) * HD;
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        e[2 * c] = qe + 32 * c + 8 * kb;
-        e[2 * c + 1] = qe + 32 * c + 8 * kb + 4;
+        qa[2 * c] = *(const float4 *)(qh0 + 32 * c + 8 * kb);
+        qa[2 * c + 1] = *(const float4 *)(qh0 + 32 * c + 8 * kb + 4);
       }
-      e[2 * NC] = ko;
-      e[2 * NC + 1] = ko + 4;
-      e[2 * NC + 2] = vo;
-      e[2 * NC + 3] = vo + 4;
       if (kvw) {
-        float4 all[2 * NC + 4];
-        if (TAG)
-          ld_tagged4(m.tqkv, e, tag_in, tw, all);
-        else
-          InPlain{m.qkv}.load4(e, all);
-#pragma unroll
-        for (int i = 0; i < 2 * NC; ++i) qa[i] = all[i];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) kva[i] = all[2 * NC + i];
+        kva[0] = *(const float4 *)(qst + nq4 * 4 + d0k);
+        kva[1] = *(const float4 *)(qst + nq4 * 4 + d0k + 4);
+        kva[2] = *(const float4 *)(qst + nq4 * 4 + HD + d0k);
+        kva[3] = *(const float4 *)(qst + nq4 * 4 + HD + d0k + 4);
       } else {
-        int eq[2 * NC];
-#pragma unroll
-        for (int i = 0; i < 2 * NC; ++i) eq[i] = e[i];
-        if (TAG)
-          ld_tagged4(m.tqkv, eq, tag_in, tw, qa);
-        else
-          InPlain{m.qkv}.load4(eq, qa);
 #pragma unroll
         for (int i = 0; i < 4; ++i) kva[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       }
