@@ -34,11 +34,31 @@ __global__ __launch_bounds__(GL3_BLOCK) void gemv_kernel(Mat W, int out_rows, co
   P::run(W, out_rows, InPlain{x}, normw, eps, OutPlain{y}, best, blockIdx.x, gridDim.x, lds);
 }
 
+// Workgroups of a GEMV kernel that fit on the device at once (occupancy with
+// the phase's LDS, times the CU count).  A workgroup stages (and normalizes)
+// the input vector once and then strides over its items, so a grid of one
+// resident round amortizes the staging over all the items it holds.
+template <class P>
+static int resident_gemv_grid(size_t lds) {
+  int dev = 0, n_cu = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                              hipSuccess)
+    return 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_kernel<P>, GL3_BLOCK, lds) != hipSuccess)
+    return 0;
+  return per_cu * n_cu;
+}
+
 template <class P>
 static hipError_t launch_gemv_t(const Mat &W, int out_rows, const float *x, const float *normw, float eps, float *y,
                                 unsigned long long *best, int grid, hipStream_t s) {
   const int items = P::items(out_rows);
-  if (grid <= 0) grid = items < 8192 ? items : 8192;
+  if (grid <= 0) {
+    // the LDS of the phase grows by a few floats per item a workgroup holds: size the occupancy query for 4 KB more
+    const int res = resident_gemv_grid<P>(P::lds_bytes(W.cols, out_rows, items, normw != nullptr) + 4096);
+    grid = res > 0 && res < items ? res : items;
+    if (grid > 8192) grid = 8192;
+  }
   size_t lds = P::lds_bytes(W.cols, out_rows, grid, normw != nullptr);
   hipLaunchKernelGGL(gemv_kernel<P>, dim3(grid), dim3(GL3_BLOCK), lds, s, W, out_rows, x, normw, eps, y, best);
   return hipGetLastError();
