@@ -1348,9 +1348,10 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
     at.pos = pos;
     at.wave = wave;
     at.lane = lane;
+    // only the first tile goes out before q is polled: reads return in issue
+    // order per CU, so every tile requested ahead of the poll delays q (and the
+    // ring, full, cannot take more); the next tiles follow once q is in
     if (ntw > 0) at.template issue<0, true>(0);
-    if (ntw > 1) at.template issue<1, true>(1);
-    if (ATT_DEPTH >= 3 && ntw > 2) at.template issue<(ATT_DEPTH >= 3 ? 2 : 1), true>(2);
 
     // ---- q of head hh (columns >= GQ stay zero), the new k and v: one round trip.
     // What does not depend on the QKV phase is requested first (RoPE table
@@ -1405,6 +1406,8 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
         *(float4 *)(qst + 4 * t) = v1[0];
       }
       __syncthreads();
+      if (ntw > 1) at.template issue<1, true>(1);
+      if (ATT_DEPTH >= 3 && ntw > 2) at.template issue<(ATT_DEPTH >= 3 ? 2 : 1), true>(2);
       // lanes of columns >= GQ take head 0 and keep zeros
       const float *qh0 = qst + (qok ? hh : 0) * HD;
 #pragma unroll

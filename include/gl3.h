@@ -164,10 +164,14 @@ int gl3_get_timing(gl3_plan *p, double *elapsed_ms, double *kernel_ms, int32_t *
 
 /* Phase trace of the last token of the persistent decode kernel (needs
  * GL3_FLAG_PHASE_TRACE): durations in microseconds, as seen by workgroup 0, of
- * embedding, 0, then per layer {QKV, 0, attention, request of the Wo weights,
- * Wo, request of the gate/up weights, gate/up, request of the down weights,
- * down, request of the next phase's weights}, then the classifier (each phase
- * includes its wait for its input).  *n_out gets the number of entries written.
+ * embedding, 0, then per layer {QKV, attention up to q/k/v read, attention
+ * tiles, attention split merge, Wo (with the request of its weights), request
+ * of the gate/up weights, gate/up, request of the down weights, down (fused
+ * FFN: down partials), request of the next phase's weights (fused FFN: and
+ * the reduce of the down partials)}, then the classifier (each phase includes
+ * its wait for its input; a workgroup without an attention item stamps the
+ * first two attention boundaries on its way through).  *n_out gets the number
+ * of entries written.
  * No reference counterpart (the reference's TornadoVM profiler times whole task
  * graphs: llama-tornado:131-134). */
 int gl3_get_phase_trace(gl3_plan *p, double *us_out, int32_t max_entries, int32_t *n_out);
