@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 
 import oracle.oracle as orc
+from gpullama3_hip import HipMasterPlan
 from gpullama3_hip import _lib as L
 from gpullama3_hip.model import synth_model
 from harness import build, prefill_kv, small, top2_margin
@@ -168,3 +169,22 @@ def test_forward_argument_errors(gpu):
         plan.forward(0, shape.context_length)
     with pytest.raises(ValueError):
         plan.generate_greedy(0, shape.context_length - 2, 5)
+
+
+def test_phase_trace_is_ordered(gpu):
+    """Phase stamps of the persistent kernel (GL3_FLAG_PHASE_TRACE): one row per
+    boundary, every workgroup's stamps advance through the token, and a traced
+    run decodes the same tokens as an untraced one."""
+    shape = small("llama1b_q8")
+    plan, ref, tensors = build(shape, flags=L.FLAG_PHASE_TRACE)
+    gen = plan.generate_greedy(17, 0, 6)
+    st = plan.phase_stamps().astype(np.int64)
+    assert st.shape[0] == 3 + 10 * shape.n_layers + 1
+    assert (np.diff(st, axis=0) >= 0).all()
+    tr = plan.phase_trace()
+    assert len(tr) == st.shape[0] - 1 and (tr >= 0).all()
+    plain = HipMasterPlan.initialize_plan(shape, tensors)
+    assert np.array_equal(plain.generate_greedy(17, 0, 6), gen)
+    plain.free_execution_plan()
+    plan.free_execution_plan()
+    ref.close()
