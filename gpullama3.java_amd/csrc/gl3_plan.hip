@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "../../include/gl3.h"
+#include "gl3_host.h"
 #include "gl3_internal.h"
 
 using namespace gl3;
@@ -23,15 +24,26 @@ using namespace gl3;
 
 static thread_local std::string g_last_error;
 
-static int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
-static int fail(int code, const char *fmt, ...) {
+static int vfail(int code, const char *fmt, va_list ap) {
   char buf[512];
-  va_list ap;
-  va_start(ap, fmt);
   vsnprintf(buf, sizeof buf, fmt, ap);
-  va_end(ap);
   g_last_error = buf;
   return code;
+}
+static int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+static int fail(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  const int r = vfail(code, fmt, ap);
+  va_end(ap);
+  return r;
+}
+int gl3::host_fail(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  const int r = vfail(code, fmt, ap);
+  va_end(ap);
+  return r;
 }
 
 #define HIP_TRY(expr)                                                                                     \

@@ -12,7 +12,7 @@ import ctypes
 import numpy as np
 
 from . import _lib as L
-from .model import ModelShape, gl3_config, kind_and_layer
+from .model import FAMILY_MODEL_TYPE, ModelShape, gl3_config, kind_and_layer
 
 
 def _raise(status):
@@ -59,6 +59,22 @@ class HipMasterPlan:
         except BaseException:
             plan.free_execution_plan()
             raise
+        return plan
+
+    # -- ModelLoader.loadModel + initializeTornadoVMPlan, done by the library from a path
+    @classmethod
+    def from_gguf(cls, path, context_length=-1, flags=0):
+        """Plan built straight from a GGUF file (gl3_create_from_gguf): the library
+        parses it, maps it read-only and uploads every tensor from the mapping."""
+        cfg = gguf_config(path, context_length, flags)
+        plan = cls.__new__(cls)
+        plan.lib = L.load()
+        plan.shape = shape_of_config(cfg)
+        plan.flags = flags
+        h = ctypes.c_void_p()
+        _ok(plan.lib.gl3_create_from_gguf(str(path).encode(), context_length, flags, ctypes.byref(h)))
+        plan.h = h
+        plan._logits = np.zeros(plan.shape.vocab_size, dtype=np.float32)
         return plan
 
     def upload(self, name, ggml_type, data):
@@ -152,6 +168,22 @@ class HipMasterPlan:
             self.free_execution_plan()
         except Exception:
             pass
+
+
+def gguf_config(path, context_length=-1, flags=0):
+    """gl3_config the library derives from a GGUF file (gl3_gguf_config; no GPU needed)."""
+    cfg = L.Gl3Config()
+    _ok(L.load().gl3_gguf_config(str(path).encode(), context_length, flags, ctypes.byref(cfg)))
+    return cfg
+
+
+def shape_of_config(cfg):
+    """ModelShape of a gl3_config (the embedding type is not part of the config:
+    it is taken to be the planner key, and tying is left unknown as False)."""
+    family = {v: k for k, v in FAMILY_MODEL_TYPE.items()}.get(cfg.model_type, "llama")
+    return ModelShape(family, cfg.dim, cfg.hidden_dim, cfg.n_layers, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim,
+                      cfg.vocab_size, cfg.context_length, cfg.rms_norm_eps, cfg.rope_theta, cfg.weight_type,
+                      cfg.weight_type, False, "")
 
 
 def device_name():

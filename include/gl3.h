@@ -182,6 +182,28 @@ int gl3_get_phase_trace(gl3_plan *p, double *us_out, int32_t max_entries, int32_
  * start at i = 0).  Needs GL3_FLAG_PHASE_TRACE.  No reference counterpart. */
 int gl3_get_phase_stamps(gl3_plan *p, uint64_t *out, int64_t max_entries, int32_t *n_stamps, int32_t *n_workgroups);
 
+/* The configuration of a GGUF model file, as the reference derives it: header
+ * and metadata as GGUF.loadGGUFMetadata reads them (tensor/GGUF.java:43-92,
+ * versions 2 and 3), the family from general.name as
+ * ModelLoader.detectModelType (model/loader/ModelLoader.java:45-67), the shape
+ * from the <arch>.* keys as the loaders' createConfiguration
+ * (LlamaModelLoader.java:47-62, MistralModelLoader.java:44-66,
+ * Qwen3ModelLoader.java:48-73, Phi3ModelLoader.java:45-60), and the planner
+ * key from the type of output.weight (token_embd.weight when tied,
+ * AbstractModelLoader.java:146-150).  context_length is the reference's
+ * -n/--max-tokens: < 0 keeps the model's own for Llama, Mistral and Qwen3
+ * (Mistral and Qwen3 take the smaller of the two); Phi-3 needs it > 0, as its
+ * loader uses the requested value as is.  Reads the file only: no GPU call. */
+int gl3_gguf_config(const char *path, int32_t context_length, uint32_t flags, gl3_config *cfg_out);
+
+/* gl3_gguf_config, gl3_create, one gl3_upload per tensor straight from a
+ * read-only mapping of the file (no host copy; rope_freqs.weight and tensors
+ * this path does not read are skipped, GGUF.java:120-123), then gl3_prepare:
+ * the reference's ModelLoader.loadModel (ModelLoader.java:81-92) followed by
+ * the weight copy-in of initializeTornadoVMPlan (TornadoVMMasterPlan.java:37-79),
+ * for callers that hand the library a path. */
+int gl3_create_from_gguf(const char *path, int32_t context_length, uint32_t flags, gl3_plan **out);
+
 /* Replaces freeTornadoExecutionPlan (TornadoVMMasterPlan.java:200-202). */
 void gl3_destroy(gl3_plan *p);
 

@@ -12,6 +12,7 @@ import pytest
 import oracle.oracle as orc
 from gpullama3_hip import HipMasterPlan
 from gpullama3_hip import _lib as L
+from gpullama3_hip.gguf import write_gguf
 from gpullama3_hip.model import synth_model
 from harness import build, prefill_kv, small, top2_margin
 
@@ -188,3 +189,25 @@ def test_phase_trace_is_ordered(gpu):
     plain.free_execution_plan()
     plan.free_execution_plan()
     ref.close()
+
+
+@pytest.mark.parametrize("key", ["llama1b_q8", "llama1b_f16", "qwen3_06b_q8", "phi3_mini_f16"])
+def test_plan_from_gguf_matches_upload(gpu, tmp_path, key):
+    """gl3_create_from_gguf (the library parses the file, maps it and uploads from
+    the mapping) gives bit-identical logits to uploading the same tensors."""
+    shape = small(key)
+    if key == "llama1b_f16":
+        shape = shape.with_(tied=True)
+    print(f"[case] {key} from GGUF", flush=True)
+    tensors = synth_model(shape, 7, norm_init="random")
+    path = tmp_path / "m.gguf"
+    write_gguf(path, shape, tensors)
+    a = HipMasterPlan.initialize_plan(shape, tensors)
+    b = HipMasterPlan.from_gguf(path, shape.context_length)
+    assert b.shape.vocab_size == shape.vocab_size and b.shape.n_layers == shape.n_layers
+    for pos, tok in enumerate([3, 1000, 77, 4095]):
+        la, ta = a.forward(tok, pos)
+        lb, tb = b.forward(tok, pos)
+        assert np.array_equal(la, lb) and ta == tb, pos
+    a.free_execution_plan()
+    b.free_execution_plan()
