@@ -226,6 +226,16 @@ typedef Shape<FMT_Q8,  1024, 2048, 1024,  3072, 128, 2, 8, 3, Tile<1, 1, 4>, Til
 typedef Shape<FMT_F16, 3072, 3072, 3072,  8192,  96, 1, 8, 3, Tile<6, 1, 1>, Tile<6, 1, 1>, Tile<3, 2, 1>, Tile<4, 4, 2>, Tile<6, 1, 1>> ShapePhi3MiniF16;
 typedef Shape<FMT_Q8,  4096, 4096, 1024, 14336, 128, 4, 8, 2, Tile<4, 1, 2>, Tile<4, 1, 2>, Tile<4, 1, 1>, Tile<7, 2, 1>, Tile<4, 1, 2>> ShapeLlama8BQ8;
 
+// The first slot-load of the fused FFN's Wdown slice, requested into ring slot
+// 2 (unused by the gate/up phase) once gate/up's last weight slot has arrived,
+// so it streams while gate/up finishes.
+template <class DS>
+struct DownSliceFirstHalf {
+  Mat W;
+  int rows, slice;
+  __device__ __forceinline__ void operator()() { DS::template issue<2>(W, rows, slice, 0); }
+};
+
 // n_steps greedy decode steps in one launch: per step embedding, L x (QKV,
 // attention, Wo, gate/up, down), classifier.  Inside a step no phase waits at
 // a barrier: each reads its input vector as tagged cells and waits only for
@@ -282,12 +292,15 @@ __global__ __launch_bounds__(GL3_STEP_BLOCK, 1) void decode_step_kernel(ModelDev
       if constexpr (SH::ffn == 1) {
         // fused FFN: this workgroup's 32 SwiGLU rows stay in LDS and meet its
         // 32-column slice of Wdown; t_hb tags the partial sums
+        const Mat wds = ld_mat(&L->down_sl);
         SH::GU::run(ld_mat(&L->gu), SH::hidden, InTag{m.txb, t_wo, tw}, L->ffn_norm, m.eps, OutNone{}, nullptr, blk,
-                    nblk, lds, true);
+                    nblk, lds, true, DownSliceFirstHalf<typename SH::DS>{wds, SH::dim, blk});
+        // the first half went out with gate/up's last slot (every workgroup holds gate/up items)
         trace(m, tk++);
-        SH::DS::prefetch(ld_mat(&L->down_sl), SH::dim, blk);
+        SH::DS::template issue<0>(wds, SH::dim, blk, 1);
         trace(m, tk++);
-        SH::DS::run(SH::dim, lds + SH::GU::obuf_offset(SH::dim, true), m.tdp + (size_t)blk * SH::dim, t_hb);
+        SH::DS::template run<2, 0>(SH::dim, lds + SH::GU::obuf_offset(SH::dim, true), m.tdp + (size_t)blk * SH::dim,
+                                   t_hb);
         trace(m, tk++);
         if (l + 1 < m.n_layers)
           SH::QKV::prefetch(ld_mat(&layers[l + 1].qkv), rows_qkv, blk, nblk);

@@ -511,6 +511,13 @@ __device__ __forceinline__ void dma4(dma_rsrc_t r, void *lds, unsigned voff, uns
                : "memory", "m0");
 }
 
+// Loads a GEMV phase may request for the phase after it once its own last
+// slot has arrived (so they do not delay its waits): called at most once, after
+// the wait for the last slot and before that slot's dot products.
+struct NoTail {
+  __device__ __forceinline__ void operator()() {}
+};
+
 // MAP 0: workgroup blk takes items blk, blk + nblk, ...; MAP 1: the items are
 // split into nblk contiguous runs (the host checks that nblk divides them).
 template <int FMT, int KC, int KS, int NR, int MODE, int BS, int SC_ = 0, int DEPTH = 2, int MAP = 0>
@@ -704,9 +711,10 @@ struct GemvPhase {
     }
   }
 
-  template <int S>
+  template <int S, class TAIL>
   static __device__ __forceinline__ void step(const Mat &W, int out_rows, int u, int nu, int blk, int nblk,
-                                              const XSlice &xr, float (&acc)[NR][NP], float *kpart, float *obuf) {
+                                              const XSlice &xr, float (&acc)[NR][NP], float *kpart, float *obuf,
+                                              TAIL &tail) {
     if (u < nu) {
       // slot S is complete once at most the loads of the (up to DEPTH-1) later slot-loads are outstanding
       const int later = nu - 1 - u;
@@ -714,8 +722,10 @@ struct GemvPhase {
         wait_vmem<2 * NI_MIN>();
       else if (later >= 1)
         wait_vmem<NI_MIN>();
-      else
+      else {
         wait_vmem<0>();
+        tail();
+      }
       const int pass = PASSES > 1 ? u % PASSES : 0;
       dot_slot<S>(xr, pass, acc);
       if (u + DEPTH < nu) issue<S>(W, out_rows, u + DEPTH, blk, nblk);
@@ -746,9 +756,10 @@ struct GemvPhase {
   // MODE_LOGITS, y gets the rows and best_out[blk] the argmax key of the rows
   // this workgroup produced.  prefetched: prefetch() was already called with
   // the same W, out_rows, blk and nblk.
-  template <class IN, class OUT>
+  template <class IN, class OUT, class TAIL = NoTail>
   static __device__ void run(const Mat &W, int out_rows, const IN &x, const float *normw, float eps, const OUT &y,
-                             unsigned long long *best_out, int blk, int nblk, float *lds, bool prefetched = false) {
+                             unsigned long long *best_out, int blk, int nblk, float *lds, bool prefetched = false,
+                             TAIL tail = TAIL{}) {
     const int K = W.cols;
     const bool stg = staged(normw != nullptr);
     float *xs = lds;                          // K floats when staged
@@ -815,9 +826,9 @@ struct GemvPhase {
 #pragma unroll
       for (int p = 0; p < NP; ++p) acc[r][p] = 0.0f;
     for (int u = 0; u < nu; u += DEPTH) {
-      step<0>(W, out_rows, u, nu, blk, nblk, xr, acc, kpart, obuf);
-      step<1>(W, out_rows, u + 1, nu, blk, nblk, xr, acc, kpart, obuf);
-      if (DEPTH == 3) step<(DEPTH == 3 ? 2 : 1)>(W, out_rows, u + 2, nu, blk, nblk, xr, acc, kpart, obuf);
+      step<0>(W, out_rows, u, nu, blk, nblk, xr, acc, kpart, obuf, tail);
+      step<1>(W, out_rows, u + 1, nu, blk, nblk, xr, acc, kpart, obuf, tail);
+      if (DEPTH == 3) step<(DEPTH == 3 ? 2 : 1)>(W, out_rows, u + 2, nu, blk, nblk, xr, acc, kpart, obuf, tail);
     }
     __syncthreads();
 
@@ -928,6 +939,8 @@ struct DownSliceQ8 {
     issue<0>(W, rows, slice, 0);
     issue<1>(W, rows, slice, 1);
   }
+  // SA, SB: the ring slots holding the first and the second slot-load
+  template <int SA = 0, int SB = 1>
   static __device__ __forceinline__ void run(int rows, const float *hb_lds, uint2 *dst, unsigned tag) {
     const int lane = lane_id();
     float hv[16];
@@ -944,9 +957,9 @@ struct DownSliceQ8 {
     // two slot-loads (dim 2048); stores only after both, so the waits count loads alone
     float p0[8], p1[8];
     wait_vmem<NI>();
-    compute<0>(hv, p0);
+    compute<SA>(hv, p0);
     wait_vmem<0>();
-    compute<1>(hv, p1);
+    compute<SB>(hv, p1);
     if ((lane & 1) == 0) {
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
