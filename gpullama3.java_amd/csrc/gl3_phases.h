@@ -71,7 +71,8 @@ struct DecodeState {
   int parity;     // which half of best[] this step writes
   int step;       // steps run since the start of the current generate call
   int nbest;      // number of entries per half of best[]
-  int pad[2];
+  int n_prompt;   // steps 0 .. n_prompt-1 forward the prompt tokens (prompt[step]); later steps the argmax
+  int pad;
 };
 
 struct ModelDev {
@@ -103,6 +104,7 @@ struct ModelDev {
   unsigned long long *best; // argmax keys [2][nbest]
   DecodeState *st;
   int *tokens_out;          // device copy of generated tokens
+  const int *prompt;        // prompt tokens of the current generate call [context length]
   unsigned long long *tstamp;  // optional phase trace: s_memrealtime at each phase boundary, per workgroup
 };
 
@@ -116,7 +118,7 @@ __device__ __forceinline__ void trace(const ModelDev &m, int idx) {
 // ------------------------------------------------------------ step control
 
 struct StepInfo {
-  int pos, token, from_best, parity, step, nbest;
+  int pos, token, from_best, parity, step, nbest, n_prompt;
 };
 
 // Orderable key of (value, row): larger value wins, then the smaller row, as in
@@ -132,7 +134,7 @@ __device__ __forceinline__ int argmax_key_row(unsigned long long k) { return (in
 __device__ inline StepInfo read_step(const ModelDev &m, int *lds_i) {
   if (threadIdx.x < GL3_WAVE) {
     const int *s = (const int *)m.st;
-    int v = threadIdx.x < 6 ? ld_coherent_i32(s + threadIdx.x) : 0;
+    int v = threadIdx.x < 7 ? ld_coherent_i32(s + threadIdx.x) : 0;
     int from_best = __shfl(v, 2), parity = __shfl(v, 3), nbest = __shfl(v, 5);
     unsigned long long best = 0;
     if (from_best) {
@@ -152,7 +154,7 @@ __device__ inline StepInfo read_step(const ModelDev &m, int *lds_i) {
         best = other > best ? other : best;
       }
     }
-    if (threadIdx.x < 6) lds_i[threadIdx.x] = v;
+    if (threadIdx.x < 7) lds_i[threadIdx.x] = v;
     if (threadIdx.x == 0 && from_best) {
       int row = argmax_key_row(best);
       lds_i[1] = (row >= 0 && row < m.vocab) ? row : 0;  // an empty key set cannot index past the table
@@ -166,6 +168,7 @@ __device__ inline StepInfo read_step(const ModelDev &m, int *lds_i) {
   si.parity = lds_i[3];
   si.step = lds_i[4];
   si.nbest = lds_i[5];
+  si.n_prompt = lds_i[6];
   __syncthreads();
   return si;
 }
@@ -176,7 +179,15 @@ __device__ inline void advance_step(const ModelDev &m, const StepInfo &si) {
     if (si.from_best && si.step > 0) m.tokens_out[si.step - 1] = si.token;
     int *s = (int *)m.st;
     __hip_atomic_store(s + 0, si.pos + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(s + 2, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the next step forwards the next prompt token while the prompt lasts
+    // (InferenceEngine.java:83-131: prompt tokens are forced, their logits unused), then the argmax
+    const int next = si.step + 1;
+    if (next < si.n_prompt) {
+      __hip_atomic_store(s + 1, m.prompt[next], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(s + 2, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      __hip_atomic_store(s + 2, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     __hip_atomic_store(s + 3, si.parity ^ 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(s + 4, si.step + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }

@@ -364,6 +364,11 @@ extern "C" int gl3_create(const gl3_config *cfg, gl3_plan **out) {
   TRY(dev_alloc(p, &m.best, 2 * (size_t)p->nbest));
   TRY(dev_alloc(p, &m.st, 1));
   TRY(dev_alloc(p, &m.tokens_out, (size_t)cfg->context_length));
+  {
+    int *pr = nullptr;
+    TRY(dev_alloc(p, &pr, (size_t)cfg->context_length));
+    m.prompt = pr;
+  }
   if (cfg->flags & GL3_FLAG_PHASE_TRACE) TRY(dev_alloc(p, &m.tstamp, (size_t)(4 + 10 * L) * p->n_cu));
   unsigned *bar = nullptr;
   TRY(dev_alloc(p, &bar, GL3_BAR_GROUPS * GL3_BAR_STRIDE + 64));
@@ -703,7 +708,8 @@ static void set_state(gl3_plan *p, int token, int pos) {
   s.parity = 0;
   s.step = 0;
   s.nbest = p->logits_grid;
-  s.pad[0] = s.pad[1] = 0;
+  s.n_prompt = 0;
+  s.pad = 0;
 }
 
 static hipEvent_t next_event(gl3_plan *p) {
@@ -808,6 +814,30 @@ extern "C" int gl3_generate_greedy(gl3_plan *p, int32_t token, int32_t position,
   if ((rc = run_steps(p, n_steps))) return rc;
   HIP_TRY(launch_finish(p->m, p->stream));
   HIP_TRY(hipMemcpyAsync(tokens_out, p->m.tokens_out, (size_t)n_steps * 4, hipMemcpyDeviceToHost, p->stream));
+  return finish_timing_and_errors(p);
+}
+
+extern "C" int gl3_generate_from_prompt(gl3_plan *p, const int32_t *prompt, int32_t n_prompt, int32_t position,
+                                        int32_t n_gen, int32_t *tokens_out) {
+  if (!p || !prompt || !tokens_out) return fail(GL3_ERR_INVALID_ARGUMENT, "null argument");
+  if (n_prompt <= 0 || n_gen <= 0) return fail(GL3_ERR_INVALID_ARGUMENT, "n_prompt %d and n_gen %d must be positive", n_prompt, n_gen);
+  const int64_t steps = (int64_t)n_prompt + n_gen - 1;
+  if (position < 0 || (int64_t)position + steps > p->cfg.context_length)
+    return fail(GL3_ERR_INVALID_ARGUMENT, "positions [%d, %lld) exceed context %d", position,
+                (long long)(position + steps), p->cfg.context_length);
+  for (int i = 0; i < n_prompt; ++i)
+    if (prompt[i] < 0 || prompt[i] >= p->cfg.vocab_size)
+      return fail(GL3_ERR_INVALID_ARGUMENT, "prompt token %d (index %d) out of range", prompt[i], i);
+  int rc = gl3_prepare(p);
+  if (rc) return rc;
+  HIP_TRY(hipMemcpyAsync((void *)p->m.prompt, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, p->stream));
+  set_state(p, prompt[0], position);
+  p->h_state->n_prompt = n_prompt;
+  if ((rc = run_steps(p, (int)steps))) return rc;
+  HIP_TRY(launch_finish(p->m, p->stream));
+  // the argmax after step s is recorded at tokens_out[s]; the generated ones follow the last prompt step
+  HIP_TRY(hipMemcpyAsync(tokens_out, p->m.tokens_out + (n_prompt - 1), (size_t)n_gen * 4, hipMemcpyDeviceToHost,
+                         p->stream));
   return finish_timing_and_errors(p);
 }
 

@@ -68,6 +68,7 @@ SIGNATURES = {
     "gl3_prepare": (_I, [_P]),
     "gl3_forward": (_I, [_P, ctypes.c_int32, ctypes.c_int32, _FP, _IP]),
     "gl3_generate_greedy": (_I, [_P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _IP]),
+    "gl3_generate_from_prompt": (_I, [_P, _IP, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _IP]),
     "gl3_reset": (_I, [_P]),
     "gl3_write_kv": (_I, [_P, _I, _I, _I, _U16P, _U16P]),
     "gl3_read_kv": (_I, [_P, _I, _I, _I, _U16P, _U16P]),

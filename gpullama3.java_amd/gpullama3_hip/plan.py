@@ -109,6 +109,13 @@ class HipMasterPlan:
         _ok(self.lib.gl3_generate_greedy(self.h, token, position, n_steps, L.iptr(out)))
         return out
 
+    def generate_from_prompt(self, prompt, position, n_gen):
+        """The prompt forwarded on the device, then n_gen greedy tokens (gl3_generate_from_prompt)."""
+        pr = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.zeros(n_gen, dtype=np.int32)
+        _ok(self.lib.gl3_generate_from_prompt(self.h, L.iptr(pr), pr.size, position, n_gen, L.iptr(out)))
+        return out
+
     def timing(self):
         e = ctypes.c_double()
         k = ctypes.c_double()

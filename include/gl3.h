@@ -145,6 +145,17 @@ int gl3_forward(gl3_plan *p, int32_t token, int32_t position, float *logits_out,
  * with the sampler fixed to TENSOR_ARGMAX, so the logits never leave the GPU. */
 int gl3_generate_greedy(gl3_plan *p, int32_t token, int32_t position, int32_t n_steps, int32_t *tokens_out);
 
+/* The reference's generation loop with the TENSOR_ARGMAX sampler, entirely on the
+ * device (InferenceEngine.generateTokensGPULlama, inference/InferenceEngine.java:309-355):
+ * forwards the n_prompt prompt tokens at positions position.. (their logits are
+ * not used, as in the reference's prompt phase), then greedy steps; tokens_out
+ * receives the n_gen generated tokens (the argmax after the last prompt token,
+ * then after each generated one).  n_prompt + n_gen - 1 forwards in persistent
+ * launches, no host round trip between them.  Requires every prompt token in
+ * [0, vocab_size) and position + n_prompt + n_gen - 1 <= context_length. */
+int gl3_generate_from_prompt(gl3_plan *p, const int32_t *prompt, int32_t n_prompt, int32_t position, int32_t n_gen,
+                             int32_t *tokens_out);
+
 /* Zero the KV cache (a fresh State: inference/state/LlamaState.java:61-64). */
 int gl3_reset(gl3_plan *p);
 

@@ -211,3 +211,40 @@ def test_plan_from_gguf_matches_upload(gpu, tmp_path, key):
         assert np.array_equal(la, lb) and ta == tb, pos
     a.free_execution_plan()
     b.free_execution_plan()
+
+
+@pytest.mark.parametrize("sched", sorted(SCHEDULES))
+@pytest.mark.parametrize("n_prompt,n_gen", [(1, 5), (37, 20), (200, 99)])
+def test_generate_from_prompt_matches_stepwise(gpu, sched, n_prompt, n_gen):
+    """Prompt forced then greedy on the device (one call; 200 + 99 - 1 steps cross a
+    launch boundary) equals the same loop driven token by token from the host."""
+    shape = small("llama1b_q8")
+    plan, ref, _ = build(shape, flags=SCHEDULES[sched])
+    prompt = np.random.default_rng(4).integers(0, shape.vocab_size, n_prompt)
+    start = 3
+    gen = plan.generate_from_prompt(prompt, start, n_gen)
+    plan.reset()
+    am = None
+    for i, t in enumerate(prompt):
+        _, am = plan.forward(int(t), start + i)
+    toks = [am]
+    for j in range(n_gen - 1):
+        _, am = plan.forward(toks[-1], start + n_prompt + j)
+        toks.append(am)
+    assert list(gen) == toks
+    plan.free_execution_plan()
+    ref.close()
+
+
+def test_generate_from_prompt_argument_errors(gpu):
+    shape = small("llama1b_q8")
+    plan, ref, _ = build(shape)
+    with pytest.raises(ValueError):
+        plan.generate_from_prompt([1, shape.vocab_size], 0, 4)
+    with pytest.raises(ValueError):
+        plan.generate_from_prompt([1, 2, 3], shape.context_length - 4, 3)
+    with pytest.raises(ValueError):
+        plan.generate_from_prompt([], 0, 3)
+    assert len(plan.generate_from_prompt([1, 2, 3], shape.context_length - 5, 3)) == 3
+    plan.free_execution_plan()
+    ref.close()
