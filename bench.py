@@ -194,6 +194,22 @@ def main():
             f"{seg_bytes / (km * 1e-3) / 1e9:.0f} GB/s algorithmic")
         tok = int(out[-1])
     tok_s = total_steps / wall
+    # the reference's own workload shape and count: a 128-token random prompt, then
+    # 128 greedy tokens from position 0, tokens/s = (prompt + generated) / wall time
+    # (InferenceEngine.java:134-138); prompt and generation both on the device
+    ref_wl = None
+    if args.schedule == "persistent" and shape.context_length >= 256:
+        plan.reset()
+        prompt = np.random.default_rng(args.seed).integers(0, shape.vocab_size, 128)
+        plan.generate_from_prompt(prompt, 0, 4)  # warm the path
+        plan.reset()
+        t1 = time.perf_counter()
+        plan.generate_from_prompt(prompt, 0, 128)
+        t2 = time.perf_counter()
+        ref_wl = {"prompt_tokens": 128, "generated_tokens": 128, "tok_s": round(256 / (t2 - t1), 2),
+                  "wall_ms": round(1e3 * (t2 - t1), 3),
+                  "note": "(prompt + generated) / wall time from position 0, as the reference counts its tok/s"}
+        log(f"reference workload (128 prompt + 128 greedy from position 0): {ref_wl['tok_s']} tok/s")
     # one persistent launch decodes a whole segment; per-launch figures are
     # averages over the timed launches
     avg_kernel_s = kern_ms * 1e-3 / launches
@@ -233,6 +249,7 @@ def main():
                      "kernel": kernel, "bytes_per_launch": int(avg_bytes),
                      "avg_launch_ms": round(avg_kernel_s * 1e3, 4)},
         "cpu_baseline": cpu,
+        "reference_workload": ref_wl,
     }
     print(json.dumps(rec), flush=True)
 
