@@ -123,7 +123,8 @@ def measured_traffic(cfg_key, tokens_per_launch):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed decode steps (default 256; llama8b_q8: 384, i.e. 128 at each of its three fills)")
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--config", default="llama1b_q8")
     ap.add_argument("--schedule", default="persistent", choices=["persistent", "graph"])
@@ -153,6 +154,8 @@ def main():
     from gpullama3_hip.model import CONFIGS, synth_model, tensor_specs
 
     shape = CONFIGS[args.config]
+    if args.steps is None:
+        args.steps = 384 if args.config == "llama8b_q8" else 256
     log(f"device: {device_name()}  config: {args.config} {shape}")
     t0 = time.perf_counter()
     tensors = synth_model(shape, args.seed, norm_init="ones")
