@@ -1083,10 +1083,11 @@ __host__ __device__ __forceinline__ int att_split_len(int n, int max_split, int 
 }
 
 // LDS floats of the attention phase: per-wave o [wpb][G][hd], (m, l) [wpb][G][2], a flag
-// (16 floats) and the staged q [G][hd], new k [hd] and new v [hd].
+// (16 floats), the staged q [G][hd], new k [hd] and new v [hd] twice (as read and
+// normed; prepared) and their per-group sums of squares.
 __host__ __device__ __forceinline__ int att_lds_floats(int hd, int G, int wpb, int max_split) {
   (void)max_split;
-  return wpb * G * (hd + 2) + 16 + (G + 2) * hd;
+  return wpb * G * (hd + 2) + 16 + 2 * (G + 2) * hd + (G + 2) * hd / 4;
 }
 
 __device__ __forceinline__ void f4_to(float *dst, float4 v) {
@@ -1101,42 +1102,6 @@ __device__ __forceinline__ void f4_to(float *dst, float4 v) {
 template <int NQ>
 __device__ __forceinline__ int kswz(int pos) {
   return NQ == 16 ? pos : (NQ == 8 ? (pos >> 1) : (pos >> 2));
-}
-
-// RoPE table entries of the 8 dims d0..d0+7 (Llama: entries d0/2.., 4 used;
-// NeoX: entries (d0 mod half)..).
-__device__ __forceinline__ void rope_entries(const ModelDev &m, int pos, int d0, int half, bool neox, float (&c)[8],
-                                             float (&sn)[8]) {
-  // all elements are assigned outside the branch, so the arrays stay in registers
-  const int te = neox ? (d0 < half ? d0 : d0 - half) : d0 / 2;
-  const float *cr = m.rope_cos + (size_t)pos * half + te, *ci = m.rope_sin + (size_t)pos * half + te;
-  const float4 c0 = *(const float4 *)cr, s0 = *(const float4 *)ci;
-  float4 c1 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), s1 = c1;
-  if (neox) {
-    c1 = *(const float4 *)(cr + 4);
-    s1 = *(const float4 *)(ci + 4);
-  }
-  f4_to(&c[0], c0);
-  f4_to(&c[4], c1);
-  f4_to(&sn[0], s0);
-  f4_to(&sn[4], s1);
-}
-
-// RoPE of the 8 dims d0.. of a lane: Llama pairs (2i, 2i+1) inside the lane;
-// NeoX pairs (i, i + half) with the partner values `par`.
-__device__ __forceinline__ void rope_apply(float (&v)[8], const float (&par)[8], const float (&c)[8],
-                                           const float (&sn)[8], bool neox, bool low) {
-  if (!neox) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) rope_pair(v[2 * i], v[2 * i + 1], c[i], sn[i]);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float v0 = low ? v[i] : par[i], v1 = low ? par[i] : v[i];
-      rope_pair(v0, v1, c[i], sn[i]);
-      v[i] = low ? v0 : v1;
-    }
-  }
 }
 
 __device__ __forceinline__ float inv_rms(float ss, int hd, float eps) {
@@ -1341,7 +1306,9 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
   float *opart = lds;                     // per-wave o [WPB][GQ][hd]
   float *mlp = opart + WPB * GQ * hd;     // per-wave (m, l) [WPB][GQ][2]
   int *flag = (int *)(mlp + WPB * GQ * 2);
-  float *qst = mlp + WPB * GQ * 2 + 16;   // staged q [GQ][hd], new k [hd], new v [hd]
+  float *qst = mlp + WPB * GQ * 2 + 16;   // staged q [GQ][hd], new k [hd], new v [hd] (normed, before RoPE)
+  float *qrot = qst + (GQ + 2) * HD;      // the same, prepared (normed and rotated)
+  float *ssb = qrot + (GQ + 2) * HD;      // per-group sums of squares [(GQ + 2) * hd / 4]
   const LayerDev L = ld_layer(m.layers, layer);
   const int wave = wave_id(), lane = lane_id();
   const int hh = lane % 16, kb = lane / 16;  // MFMA column (head) and k-block of this lane
@@ -1377,161 +1344,127 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
     // ring, full, cannot take more); the next tiles follow once q is in
     if (ntw > 0) at.template issue<0, true>(0);
 
-    // ---- q of head hh (columns >= GQ stay zero), the new k and v: one round trip.
-    // What does not depend on the QKV phase is requested first (RoPE table
-    // entries, Qwen3 norm weights); then q and, in the wave whose tile holds
-    // pos, the new k and v are read as one batch of tagged cells.
+    // ---- q of the GQ heads and, in the split holding pos, the new k and v:
+    // read once per workgroup (one float4 of tagged cells per staging thread,
+    // all reads in one round trip) and prepared there, once: Qwen3's per-head
+    // RMSNorm (InferenceCore.java:341-347), then RoPE (:82-100, interleaved
+    // pairs, Llama; :472-491, NeoX halves, Qwen3 / Phi-3).  A staging thread
+    // requests its RoPE entries and norm weights before it polls.  The waves
+    // then take q (and the wave whose tile holds pos the new k and v) from LDS.
     const int wpos = owns_pos ? ((pos - t0) / 16) % WPB : -1;  // wave whose tile holds pos
     const bool kvw = wave == wpos;                               // uniform over the wave
     const bool qok = hh < GQ;
-    const bool kok = lane < NQ;
-    const int d0k = 8 * (kok ? lane : 0);  // dims of the new k / v held by this lane
-    float cs[NC][8], sn[NC][8], wv[NC][8];
-    float kcs[8], ksn[8], kw[8];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const int d0 = 32 * c + 8 * kb;
-      rope_entries(m, pos, d0, half, neox, cs[c], sn[c]);
-      float4 w0 = make_float4(1.0f, 1.0f, 1.0f, 1.0f), w1 = w0;
-      if (qwen) {
-        w0 = *(const float4 *)(L.q_norm + d0);
-        w1 = *(const float4 *)(L.q_norm + d0 + 4);
-      }
-      f4_to(&wv[c][0], w0);
-      f4_to(&wv[c][4], w1);
-    }
     {
-      rope_entries(m, pos, d0k, half, neox, kcs, ksn);
-      float4 w0 = make_float4(1.0f, 1.0f, 1.0f, 1.0f), w1 = w0;
-      if (qwen) {
-        w0 = *(const float4 *)(L.k_norm + d0k);
-        w1 = *(const float4 *)(L.k_norm + d0k + 4);
+      constexpr int H4 = HD / 4;  // float4 groups per head
+      const int nq4 = GQ * H4, nst4 = nq4 + (owns_pos ? 2 * H4 : 0);
+      const int t = threadIdx.x;
+      const bool act = t < nst4;
+      const bool is_q = t < nq4, is_k = !is_q && t < nq4 + H4;
+      const bool rot = act && (is_q || is_k);  // q and k are normed (Qwen3) and rotated; v is stored as read
+      const int gi = is_q ? t : (is_k ? t - nq4 : t - nq4 - H4);  // group index within q / k / v
+      const int d = 4 * (gi % H4);                                // first dim of the group in its head
+      const int e = is_q ? kvh * GQ * HD + 4 * t
+                         : (is_k ? m.q_dim + kvh * HD + d : m.q_dim + m.kv_dim + kvh * HD + d);
+      float c4[4] = {1.0f, 1.0f, 1.0f, 1.0f}, s4[4] = {0.0f, 0.0f, 0.0f, 0.0f}, w4[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+      if (rot) {
+        // RoPE entries of the group: NeoX dims d.. use entries (d mod half)..;
+        // Llama pairs (d, d+1), (d+2, d+3) use entries d/2, d/2 + 1
+        if (neox) {
+          const int te = d < half ? d : d - half;
+          const float4 c = *(const float4 *)(m.rope_cos + (size_t)pos * half + te);
+          const float4 sv = *(const float4 *)(m.rope_sin + (size_t)pos * half + te);
+          c4[0] = c.x; c4[1] = c.y; c4[2] = c.z; c4[3] = c.w;
+          s4[0] = sv.x; s4[1] = sv.y; s4[2] = sv.z; s4[3] = sv.w;
+        } else {
+          const float2 c = *(const float2 *)(m.rope_cos + (size_t)pos * half + d / 2);
+          const float2 sv = *(const float2 *)(m.rope_sin + (size_t)pos * half + d / 2);
+          c4[0] = c.x; c4[1] = c.y;
+          s4[0] = sv.x; s4[1] = sv.y;
+        }
+        if (qwen) {
+          const float4 w = *(const float4 *)((is_q ? L.q_norm : L.k_norm) + d);
+          w4[0] = w.x; w4[1] = w.y; w4[2] = w.z; w4[3] = w.w;
+        }
       }
-      f4_to(&kw[0], w0);
-      f4_to(&kw[4], w1);
-    }
-    float4 qa[2 * NC], kva[4];
-    {
-      // q of the kv head's GQ heads and, in the split holding pos, the new k
-      // and v are read once per workgroup, one float4 of tagged cells per
-      // thread (all reads of the workgroup in one round trip), staged in LDS
-      // and then taken by every wave: reading them per lane would poll each
-      // cell up to 16 times (4 waves x the 16 MFMA columns).
-      const int nq4 = GQ * HD / 4, nst4 = nq4 + (owns_pos ? HD / 2 : 0);
-      for (int t = threadIdx.x; t < nst4; t += BS) {
-        const int e1[1] = {t < nq4 ? kvh * GQ * HD + 4 * t
-                                   : (t < nq4 + HD / 4 ? m.q_dim + kvh * HD + 4 * (t - nq4)
-                                                       : m.q_dim + m.kv_dim + kvh * HD + 4 * (t - nq4 - HD / 4))};
+      float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (act) {
+        const int e1[1] = {e};
         float4 v1[1];
         if (TAG)
           ld_tagged4(m.tqkv, e1, tag_in, tw, v1);
         else
           InPlain{m.qkv}.load4(e1, v1);
-        *(float4 *)(qst + 4 * t) = v1[0];
+        v = v1[0];
       }
+      if (qwen) {
+        // per-head sum of squares: the group partials in dim order
+        if (act) ssb[t] = ((v.x * v.x + v.y * v.y) + v.z * v.z) + v.w * v.w;
+        __syncthreads();
+        if (rot) {
+          const int h0 = t - gi % H4;
+          float ss = 0.0f;
+          for (int i = 0; i < H4; ++i) ss += ssb[h0 + i];
+          const float si = inv_rms(ss, HD, m.eps);
+          v.x = w4[0] * (si * v.x);
+          v.y = w4[1] * (si * v.y);
+          v.z = w4[2] * (si * v.z);
+          v.w = w4[3] * (si * v.w);
+        }
+      }
+      if (neox) {
+        // the partner of dim d is d +- half, in group gi +- H4/2 of the same head
+        if (act) *(float4 *)(qst + 4 * t) = v;
+        __syncthreads();
+        if (rot) {
+          const bool low = d < half;
+          const float4 pv = *(const float4 *)(qst + 4 * (low ? t + H4 / 2 : t - H4 / 2));
+          float vv[4] = {v.x, v.y, v.z, v.w};
+          const float pp[4] = {pv.x, pv.y, pv.z, pv.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float v0 = low ? vv[i] : pp[i], v1 = low ? pp[i] : vv[i];
+            rope_pair(v0, v1, c4[i], s4[i]);
+            vv[i] = low ? v0 : v1;
+          }
+          v = make_float4(vv[0], vv[1], vv[2], vv[3]);
+        }
+      } else if (rot) {
+        rope_pair(v.x, v.y, c4[0], s4[0]);
+        rope_pair(v.z, v.w, c4[1], s4[1]);
+      }
+      if (act) *(float4 *)(qrot + 4 * t) = v;
       __syncthreads();
       if (ntw > 1) at.template issue<1, true>(1);
       if (ATT_DEPTH >= 3 && ntw > 2) at.template issue<(ATT_DEPTH >= 3 ? 2 : 1), true>(2);
-      // lanes of columns >= GQ take head 0 and keep zeros
-      const float *qh0 = qst + (qok ? hh : 0) * HD;
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        qa[2 * c] = *(const float4 *)(qh0 + 32 * c + 8 * kb);
-        qa[2 * c + 1] = *(const float4 *)(qh0 + 32 * c + 8 * kb + 4);
-      }
-      if (kvw) {
-        kva[0] = *(const float4 *)(qst + nq4 * 4 + d0k);
-        kva[1] = *(const float4 *)(qst + nq4 * 4 + d0k + 4);
-        kva[2] = *(const float4 *)(qst + nq4 * 4 + HD + d0k);
-        kva[3] = *(const float4 *)(qst + nq4 * 4 + HD + d0k + 4);
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) kva[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      }
     }
     if (tk >= 0 && item == blk) trace(m, tk);
-    float qv[NC][8];
+    // q of head hh (columns >= GQ take head 0 and keep zeros) as fp16 hi + lo
+    half8 qh[NC], ql[NC];
     {
-      float ss = 0.0f;
+      const float *qh0 = qrot + (qok ? hh : 0) * HD;
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        f4_to(&qv[c][0], qa[2 * c]);
-        f4_to(&qv[c][4], qa[2 * c + 1]);
+        float qv[8];
+        f4_to(&qv[0], *(const float4 *)(qh0 + 32 * c + 8 * kb));
+        f4_to(&qv[4], *(const float4 *)(qh0 + 32 * c + 8 * kb + 4));
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          qv[c][i] = qok ? qv[c][i] : 0.0f;
-          ss += qv[c][i] * qv[c][i];
+          const float x = qok ? qv[i] : 0.0f;
+          const _Float16 h16 = (_Float16)x;
+          qh[c][i] = h16;
+          ql[c][i] = (_Float16)(x - (float)h16);
         }
-      }
-      if (qwen) {
-        const float si = inv_rms(xrow_sum(ss), hd, m.eps);
-#pragma unroll
-        for (int c = 0; c < NC; ++c)
-#pragma unroll
-          for (int i = 0; i < 8; ++i) qv[c][i] = wv[c][i] * (si * qv[c][i]);
-      }
-      if (neox) {
-        // partner dims (d +- hd/2) are exchanged through this wave's part of the
-        // partial buffer (unused until the end of the item); one wave, so the
-        // reads see the writes
-        float *xs = opart + wave * GQ * hd + (qok ? hh : 0) * hd;
-        if (qok) {
-#pragma unroll
-          for (int c = 0; c < NC; ++c) {
-            const int d0 = 32 * c + 8 * kb;
-            *(float4 *)(xs + d0) = make_float4(qv[c][0], qv[c][1], qv[c][2], qv[c][3]);
-            *(float4 *)(xs + d0 + 4) = make_float4(qv[c][4], qv[c][5], qv[c][6], qv[c][7]);
-          }
-        }
-        __builtin_amdgcn_wave_barrier();
-        asm volatile("" ::: "memory");
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          const int d0 = 32 * c + 8 * kb, pd = d0 < half ? d0 + half : d0 - half;
-          float par[8];
-          f4_to(&par[0], *(const float4 *)(xs + pd));
-          f4_to(&par[4], *(const float4 *)(xs + pd + 4));
-          rope_apply(qv[c], par, cs[c], sn[c], true, d0 < half);
-#pragma unroll
-          for (int i = 0; i < 8; ++i) qv[c][i] = qok ? qv[c][i] : 0.0f;
-        }
-        __builtin_amdgcn_wave_barrier();
-        asm volatile("" ::: "memory");
-      } else {
-#pragma unroll
-        for (int c = 0; c < NC; ++c) rope_apply(qv[c], qv[c], cs[c], sn[c], false, true);
       }
     }
-    half8 qh[NC], ql[NC];
-#pragma unroll
-    for (int c = 0; c < NC; ++c)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const _Float16 h16 = (_Float16)qv[c][i];
-        qh[c][i] = h16;
-        ql[c][i] = (_Float16)(qv[c][i] - (float)h16);
-      }
-    // new k, v (fp16 bits) of the 8 dims 8*lane.. held by lanes < NQ
+    // new k, v (fp16 bits) of the 8 dims 8*lane.. held by lanes < NQ of the wave whose tile holds pos
     unsigned knb[4] = {0u, 0u, 0u, 0u}, vnb[4] = {0u, 0u, 0u, 0u};
     if (kvw) {
-      float kv[8], vv[8], par[8];
-      float ss = 0.0f;
-      f4_to(&kv[0], kva[0]);
-      f4_to(&kv[4], kva[1]);
-      f4_to(&vv[0], kva[2]);
-      f4_to(&vv[4], kva[3]);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) ss += kok ? kv[i] * kv[i] : 0.0f;
-      if (qwen) {
-        const float si = inv_rms(row16_sum(ss), hd, m.eps);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) kv[i] = kw[i] * (si * kv[i]);
-      }
-      // NeoX partner dims d +- hd/2 live in lane +- hd/16
-      const int pl = d0k < half ? lane + half / 8 : lane - half / 8;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) par[i] = __shfl(kv[i], pl < 0 ? 0 : pl);
-      rope_apply(kv, par, kcs, ksn, neox, d0k < half);
+      const int d0k = 8 * (lane < NQ ? lane : 0);
+      float kv[8], vv[8];
+      f4_to(&kv[0], *(const float4 *)(qrot + GQ * HD + d0k));
+      f4_to(&kv[4], *(const float4 *)(qrot + GQ * HD + d0k + 4));
+      f4_to(&vv[0], *(const float4 *)(qrot + (GQ + 1) * HD + d0k));
+      f4_to(&vv[4], *(const float4 *)(qrot + (GQ + 1) * HD + d0k + 4));
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         knb[i] = (unsigned)f2h(kv[2 * i]) | ((unsigned)f2h(kv[2 * i + 1]) << 16);
