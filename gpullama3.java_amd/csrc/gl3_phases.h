@@ -766,7 +766,8 @@ struct GemvPhase {
   // weights or nullptr; y: output (MODE_RESIDUAL: y += W n(x)); for
   // MODE_LOGITS, y gets the rows and best_out[blk] the argmax key of the rows
   // this workgroup produced.  prefetched: prefetch() was already called with
-  // the same W, out_rows, blk and nblk.
+  // the same W, out_rows, blk and nblk.  tail: requests for a following phase,
+  // made once, when the last weight slot has arrived (see NoTail).
   template <class IN, class OUT, class TAIL = NoTail>
   static __device__ void run(const Mat &W, int out_rows, const IN &x, const float *normw, float eps, const OUT &y,
                              unsigned long long *best_out, int blk, int nblk, float *lds, bool prefetched = false,
