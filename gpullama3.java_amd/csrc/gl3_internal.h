@@ -39,6 +39,8 @@ hipError_t launch_f16_to_f32(const uint16_t *in, size_t n, float *out, hipStream
 hipError_t launch_fill_normal_f16(uint16_t *dst, size_t rows, size_t cols, size_t stride, unsigned long long seed,
                                   hipStream_t st);
 hipError_t launch_vt_copy(uint16_t *vt, uint16_t *rows, int hd, int pos0, int npos, bool to_vt, hipStream_t st);
+hipError_t launch_kv_rows(uint16_t *kc, uint16_t *vc, uint16_t *rk, uint16_t *rv, int n_kv, int hd, int ctxp, int pos0,
+                          int npos, bool to_cache, hipStream_t st);
 hipError_t launch_fill_normal_vt(uint16_t *vt, int hd, int npos, unsigned long long seed, hipStream_t st);
 
 }  // namespace gl3

@@ -475,6 +475,24 @@ __global__ void vt_copy_kernel(uint16_t *vt, uint16_t *rows, int hd, int pos0, i
       rows[i] = *v;
   }
 }
+// One layer's K / V cache <-> position-major rows [npos][n_kv * hd] of positions
+// pos0 .. pos0 + npos - 1 (the reference's [pos][kvDim] order).
+__global__ void kv_rows_kernel(uint16_t *kc, uint16_t *vc, uint16_t *rk, uint16_t *rv, int n_kv, int hd, int ctxp,
+                               int pos0, int npos, int to_cache) {
+  const size_t kv_dim = (size_t)n_kv * hd, n = (size_t)npos * kv_dim;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    const int t = (int)(i / kv_dim), c = (int)(i % kv_dim), h = c / hd, d = c % hd;
+    uint16_t *k = kc + ((size_t)h * ctxp + pos0 + t) * hd + d;
+    uint16_t *v = vc + (size_t)h * hd * ctxp + vt_index(pos0 + t, d, hd);
+    if (to_cache) {
+      *k = rk[i];
+      *v = rv[i];
+    } else {
+      rk[i] = *k;
+      rv[i] = *v;
+    }
+  }
+}
 // N(0,1) history for positions 0..npos-1 of one kv head's V region (draw d * npos + t)
 __global__ void fill_normal_vt_kernel(uint16_t *vt, int hd, int npos, unsigned long long seed) {
   const size_t n = (size_t)npos * hd;
@@ -522,6 +540,15 @@ hipError_t launch_vt_copy(uint16_t *vt, uint16_t *rows, int hd, int pos0, int np
   if (grid > 65536) grid = 65536;
   if (grid == 0) grid = 1;
   hipLaunchKernelGGL(vt_copy_kernel, dim3((unsigned)grid), dim3(256), 0, st, vt, rows, hd, pos0, npos, to_vt ? 1 : 0);
+  return hipGetLastError();
+}
+hipError_t launch_kv_rows(uint16_t *kc, uint16_t *vc, uint16_t *rk, uint16_t *rv, int n_kv, int hd, int ctxp, int pos0,
+                          int npos, bool to_cache, hipStream_t st) {
+  size_t grid = ((size_t)npos * n_kv * hd + 255) / 256;
+  if (grid > 65536) grid = 65536;
+  if (grid == 0) grid = 1;
+  hipLaunchKernelGGL(kv_rows_kernel, dim3((unsigned)grid), dim3(256), 0, st, kc, vc, rk, rv, n_kv, hd, ctxp, pos0, npos,
+                     to_cache ? 1 : 0);
   return hipGetLastError();
 }
 hipError_t launch_fill_normal_vt(uint16_t *vt, int hd, int npos, unsigned long long seed, hipStream_t st) {

@@ -1357,83 +1357,120 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
     const bool qok = hh < GQ;
     {
       constexpr int H4 = HD / 4;  // float4 groups per head
+      // staging threads hold group t (and t + BS when the group's q/k/v take more
+      // float4 groups than the workgroup has threads: head_dim 128 with 8 heads)
+      constexpr int NG = ((GQ + 2) * H4 + BS - 1) / BS;
       const int nq4 = GQ * H4, nst4 = nq4 + (owns_pos ? 2 * H4 : 0);
-      const int t = threadIdx.x;
-      const bool act = t < nst4;
-      const bool is_q = t < nq4, is_k = !is_q && t < nq4 + H4;
-      const bool rot = act && (is_q || is_k);  // q and k are normed (Qwen3) and rotated; v is stored as read
-      const int gi = is_q ? t : (is_k ? t - nq4 : t - nq4 - H4);  // group index within q / k / v
-      const int d = 4 * (gi % H4);                                // first dim of the group in its head
-      const int e = is_q ? kvh * GQ * HD + 4 * t
-                         : (is_k ? m.q_dim + kvh * HD + d : m.q_dim + m.kv_dim + kvh * HD + d);
-      float c4[4] = {1.0f, 1.0f, 1.0f, 1.0f}, s4[4] = {0.0f, 0.0f, 0.0f, 0.0f}, w4[4] = {1.0f, 1.0f, 1.0f, 1.0f};
-      if (rot) {
-        // RoPE entries of the group: NeoX dims d.. use entries (d mod half)..;
-        // Llama pairs (d, d+1), (d+2, d+3) use entries d/2, d/2 + 1
-        if (neox) {
-          const int te = d < half ? d : d - half;
-          const float4 c = *(const float4 *)(m.rope_cos + (size_t)pos * half + te);
-          const float4 sv = *(const float4 *)(m.rope_sin + (size_t)pos * half + te);
-          c4[0] = c.x; c4[1] = c.y; c4[2] = c.z; c4[3] = c.w;
-          s4[0] = sv.x; s4[1] = sv.y; s4[2] = sv.z; s4[3] = sv.w;
-        } else {
-          const float2 c = *(const float2 *)(m.rope_cos + (size_t)pos * half + d / 2);
-          const float2 sv = *(const float2 *)(m.rope_sin + (size_t)pos * half + d / 2);
-          c4[0] = c.x; c4[1] = c.y;
-          s4[0] = sv.x; s4[1] = sv.y;
+      bool act[NG], rot[NG], is_q[NG];
+      int tg[NG], gi[NG], d[NG];
+      float c4[NG][4], s4[NG][4], w4[NG][4];
+      float4 v[NG];
+#pragma unroll
+      for (int r = 0; r < NG; ++r) {
+        const int t = (int)threadIdx.x + r * BS;
+        tg[r] = t;
+        act[r] = t < nst4;
+        is_q[r] = t < nq4;
+        const bool is_k = !is_q[r] && t < nq4 + H4;
+        // q and k are normed (Qwen3) and rotated; v is stored as read.  Without RoPE
+        // tables (the op-level entry points) q and k are taken as given.
+        rot[r] = act[r] && (is_q[r] || is_k) && m.rope_cos != nullptr;
+        gi[r] = is_q[r] ? t : (is_k ? t - nq4 : t - nq4 - H4);  // group index within q / k / v
+        d[r] = 4 * (gi[r] % H4);                                  // first dim of the group in its head
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          c4[r][i] = 1.0f;
+          s4[r][i] = 0.0f;
+          w4[r][i] = 1.0f;
         }
-        if (qwen) {
-          const float4 w = *(const float4 *)((is_q ? L.q_norm : L.k_norm) + d);
-          w4[0] = w.x; w4[1] = w.y; w4[2] = w.z; w4[3] = w.w;
+        if (rot[r]) {
+          // RoPE entries of the group: NeoX dims d.. use entries (d mod half)..;
+          // Llama pairs (d, d+1), (d+2, d+3) use entries d/2, d/2 + 1
+          if (neox) {
+            const int te = d[r] < half ? d[r] : d[r] - half;
+            const float4 c = *(const float4 *)(m.rope_cos + (size_t)pos * half + te);
+            const float4 sv = *(const float4 *)(m.rope_sin + (size_t)pos * half + te);
+            c4[r][0] = c.x; c4[r][1] = c.y; c4[r][2] = c.z; c4[r][3] = c.w;
+            s4[r][0] = sv.x; s4[r][1] = sv.y; s4[r][2] = sv.z; s4[r][3] = sv.w;
+          } else {
+            const float2 c = *(const float2 *)(m.rope_cos + (size_t)pos * half + d[r] / 2);
+            const float2 sv = *(const float2 *)(m.rope_sin + (size_t)pos * half + d[r] / 2);
+            c4[r][0] = c.x; c4[r][1] = c.y;
+            s4[r][0] = sv.x; s4[r][1] = sv.y;
+          }
+          if (qwen) {
+            const float4 w = *(const float4 *)((is_q[r] ? L.q_norm : L.k_norm) + d[r]);
+            w4[r][0] = w.x; w4[r][1] = w.y; w4[r][2] = w.z; w4[r][3] = w.w;
+          }
         }
       }
-      float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      if (act) {
-        const int e1[1] = {e};
-        float4 v1[1];
-        if (TAG)
-          ld_tagged4(m.tqkv, e1, tag_in, tw, v1);
-        else
-          InPlain{m.qkv}.load4(e1, v1);
-        v = v1[0];
+#pragma unroll
+      for (int r = 0; r < NG; ++r) {
+        v[r] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (act[r]) {
+          const int t = tg[r];
+          const int e = is_q[r] ? kvh * GQ * HD + 4 * t
+                                : (t < nq4 + H4 ? m.q_dim + kvh * HD + d[r] : m.q_dim + m.kv_dim + kvh * HD + d[r]);
+          const int e1[1] = {e};
+          float4 v1[1];
+          if (TAG)
+            ld_tagged4(m.tqkv, e1, tag_in, tw, v1);
+          else
+            InPlain{m.qkv}.load4(e1, v1);
+          v[r] = v1[0];
+        }
       }
       if (qwen) {
         // per-head sum of squares: the group partials in dim order
-        if (act) ssb[t] = ((v.x * v.x + v.y * v.y) + v.z * v.z) + v.w * v.w;
+#pragma unroll
+        for (int r = 0; r < NG; ++r)
+          if (act[r]) ssb[tg[r]] = ((v[r].x * v[r].x + v[r].y * v[r].y) + v[r].z * v[r].z) + v[r].w * v[r].w;
         __syncthreads();
-        if (rot) {
-          const int h0 = t - gi % H4;
-          float ss = 0.0f;
-          for (int i = 0; i < H4; ++i) ss += ssb[h0 + i];
-          const float si = inv_rms(ss, HD, m.eps);
-          v.x = w4[0] * (si * v.x);
-          v.y = w4[1] * (si * v.y);
-          v.z = w4[2] * (si * v.z);
-          v.w = w4[3] * (si * v.w);
-        }
+#pragma unroll
+        for (int r = 0; r < NG; ++r)
+          if (rot[r]) {
+            const int h0 = tg[r] - gi[r] % H4;
+            float ss = 0.0f;
+            for (int i = 0; i < H4; ++i) ss += ssb[h0 + i];
+            const float si = inv_rms(ss, HD, m.eps);
+            v[r].x = w4[r][0] * (si * v[r].x);
+            v[r].y = w4[r][1] * (si * v[r].y);
+            v[r].z = w4[r][2] * (si * v[r].z);
+            v[r].w = w4[r][3] * (si * v[r].w);
+          }
       }
       if (neox) {
         // the partner of dim d is d +- half, in group gi +- H4/2 of the same head
-        if (act) *(float4 *)(qst + 4 * t) = v;
-        __syncthreads();
-        if (rot) {
-          const bool low = d < half;
-          const float4 pv = *(const float4 *)(qst + 4 * (low ? t + H4 / 2 : t - H4 / 2));
-          float vv[4] = {v.x, v.y, v.z, v.w};
-          const float pp[4] = {pv.x, pv.y, pv.z, pv.w};
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            float v0 = low ? vv[i] : pp[i], v1 = low ? pp[i] : vv[i];
-            rope_pair(v0, v1, c4[i], s4[i]);
-            vv[i] = low ? v0 : v1;
+        for (int r = 0; r < NG; ++r)
+          if (act[r]) *(float4 *)(qst + 4 * tg[r]) = v[r];
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < NG; ++r)
+          if (rot[r]) {
+            const bool low = d[r] < half;
+            const float4 pv = *(const float4 *)(qst + 4 * (low ? tg[r] + H4 / 2 : tg[r] - H4 / 2));
+            float vv[4] = {v[r].x, v[r].y, v[r].z, v[r].w};
+            const float pp[4] = {pv.x, pv.y, pv.z, pv.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              float v0 = low ? vv[i] : pp[i], v1 = low ? pp[i] : vv[i];
+              rope_pair(v0, v1, c4[r][i], s4[r][i]);
+              vv[i] = low ? v0 : v1;
+            }
+            v[r] = make_float4(vv[0], vv[1], vv[2], vv[3]);
           }
-          v = make_float4(vv[0], vv[1], vv[2], vv[3]);
-        }
-      } else if (rot) {
-        rope_pair(v.x, v.y, c4[0], s4[0]);
-        rope_pair(v.z, v.w, c4[1], s4[1]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < NG; ++r)
+          if (rot[r]) {
+            rope_pair(v[r].x, v[r].y, c4[r][0], s4[r][0]);
+            rope_pair(v[r].z, v[r].w, c4[r][1], s4[r][1]);
+          }
       }
-      if (act) *(float4 *)(qrot + 4 * t) = v;
+#pragma unroll
+      for (int r = 0; r < NG; ++r)
+        if (act[r]) *(float4 *)(qrot + 4 * tg[r]) = v[r];
       __syncthreads();
       if (ntw > 1) at.template issue<1, true>(1);
       if (ATT_DEPTH >= 3 && ntw > 2) at.template issue<(ATT_DEPTH >= 3 ? 2 : 1), true>(2);

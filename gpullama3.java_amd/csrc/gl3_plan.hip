@@ -202,6 +202,7 @@ static void destroy_plan(gl3_plan *p) {
   if (p->ev_begin) (void)hipEventDestroy(p->ev_begin);
   if (p->ev_end) (void)hipEventDestroy(p->ev_end);
   for (void *a : p->allocs) (void)hipFree(a);
+  if (p->staging) (void)hipFree(p->staging);
   if (p->h_state) (void)hipHostFree(p->h_state);
   if (p->h_best) (void)hipHostFree(p->h_best);
   if (p->h_err) (void)hipHostFree(p->h_err);
@@ -690,9 +691,28 @@ extern "C" int gl3_prepare(gl3_plan *p) {
     }
   }
   p->logits_grid = p->use_step_kernel ? p->step_grid : p->nbest;
-  if (!p->use_step_kernel && !p->graph_exec) {
+  // the captured graph holds the device pointers of this preparation (the
+  // classifier of a tied plan changes when output.weight is uploaded later):
+  // capture it again on every prepare
+  if (p->graph_exec) {
+    HIP_TRY(hipGraphExecDestroy(p->graph_exec));
+    p->graph_exec = nullptr;
+  }
+  if (p->graph) {
+    HIP_TRY(hipGraphDestroy(p->graph));
+    p->graph = nullptr;
+  }
+  if (!p->use_step_kernel) {
     int rc = build_graph(p);
     if (rc) return rc;
+  }
+  // the Q8_0 upload staging buffer is not needed after the weights are in place
+  // (a later upload allocates it again)
+  if (p->staging) {
+    HIP_TRY(hipStreamSynchronize(p->stream));
+    HIP_TRY(hipFree(p->staging));
+    p->staging = nullptr;
+    p->staging_bytes = 0;
   }
   p->prepared = true;
   return GL3_OK;
@@ -857,28 +877,27 @@ static int kv_copy(gl3_plan *p, int layer, int pos0, int npos, uint16_t *host_k,
     return fail(GL3_ERR_INVALID_ARGUMENT, "kv range layer %d [%d,%d) outside the cache", layer, pos0, pos0 + npos);
   if (!host_k || !host_v) return fail(GL3_ERR_INVALID_ARGUMENT, "null buffer");
   if (npos == 0) return GL3_OK;
+  // one contiguous host copy of each of K and V through a device staging area in
+  // the host's row order, rearranged on the device (a strided copy per head into
+  // pageable host memory is orders of magnitude slower)
   const int hd = c.head_dim, nkv = c.n_kv_heads, ctxp = p->m.ctxp;
-  const hipMemcpyKind kind = to_device ? hipMemcpyHostToDevice : hipMemcpyDeviceToHost;
-  uint16_t *stage = nullptr;  // one head's V rows [npos][hd]
-  hipError_t he = hipMallocAsync((void **)&stage, (size_t)npos * hd * 2, p->stream);
+  const size_t n = (size_t)npos * p->kv_dim;
+  uint16_t *stage = nullptr;  // [2][npos][kv_dim]: K rows then V rows
+  hipError_t he = hipMallocAsync((void **)&stage, 2 * n * 2, p->stream);
   if (he != hipSuccess) return fail(GL3_ERR_OUT_OF_MEMORY, "kv staging: %s", hipGetErrorString(he));
-  int rc = GL3_OK;
-  for (int h = 0; h < nkv && rc == GL3_OK; ++h) {
-    uint16_t *kdev = p->m.kc + (((size_t)layer * nkv + h) * ctxp + pos0) * hd;
-    uint16_t *vt = p->m.vc + ((size_t)layer * nkv + h) * hd * ctxp;
-    uint16_t *hk = host_k + (size_t)h * hd, *hv = host_v + (size_t)h * hd;
-    if (to_device) {
-      he = hipMemcpy2DAsync(kdev, hd * 2, hk, (size_t)p->kv_dim * 2, hd * 2, npos, kind, p->stream);
-      if (he == hipSuccess) he = hipMemcpy2DAsync(stage, hd * 2, hv, (size_t)p->kv_dim * 2, hd * 2, npos, kind, p->stream);
-      if (he == hipSuccess) he = launch_vt_copy(vt, stage, hd, pos0, npos, true, p->stream);
-    } else {
-      he = hipMemcpy2DAsync(hk, (size_t)p->kv_dim * 2, kdev, hd * 2, hd * 2, npos, kind, p->stream);
-      if (he == hipSuccess) he = launch_vt_copy(vt, stage, hd, pos0, npos, false, p->stream);
-      if (he == hipSuccess) he = hipMemcpy2DAsync(hv, (size_t)p->kv_dim * 2, stage, hd * 2, hd * 2, npos, kind, p->stream);
-    }
-    if (he == hipSuccess) he = hipStreamSynchronize(p->stream);  // the staging buffer is reused per head
-    if (he != hipSuccess) rc = fail(GL3_ERR_DEVICE, "kv copy: %s", hipGetErrorString(he));
+  uint16_t *kl = p->m.kc + (size_t)layer * nkv * ctxp * hd, *vl = p->m.vc + (size_t)layer * nkv * ctxp * hd;
+  if (to_device) {
+    he = hipMemcpyAsync(stage, host_k, n * 2, hipMemcpyHostToDevice, p->stream);
+    if (he == hipSuccess) he = hipMemcpyAsync(stage + n, host_v, n * 2, hipMemcpyHostToDevice, p->stream);
+    if (he == hipSuccess) he = launch_kv_rows(kl, vl, stage, stage + n, nkv, hd, ctxp, pos0, npos, true, p->stream);
+  } else {
+    he = launch_kv_rows(kl, vl, stage, stage + n, nkv, hd, ctxp, pos0, npos, false, p->stream);
+    if (he == hipSuccess) he = hipMemcpyAsync(host_k, stage, n * 2, hipMemcpyDeviceToHost, p->stream);
+    if (he == hipSuccess) he = hipMemcpyAsync(host_v, stage + n, n * 2, hipMemcpyDeviceToHost, p->stream);
   }
+  int rc = GL3_OK;
+  if (he == hipSuccess) he = hipStreamSynchronize(p->stream);  // host memory is borrowed for the call only
+  if (he != hipSuccess) rc = fail(GL3_ERR_DEVICE, "kv copy: %s", hipGetErrorString(he));
   he = hipFreeAsync(stage, p->stream);
   if (he == hipSuccess) he = hipStreamSynchronize(p->stream);
   if (he != hipSuccess && rc == GL3_OK) rc = fail(GL3_ERR_DEVICE, "kv copy: %s", hipGetErrorString(he));
@@ -954,6 +973,36 @@ extern "C" int gl3_get_timing(gl3_plan *p, double *elapsed_ms, double *kernel_ms
   if (elapsed_ms) *elapsed_ms = p->last_elapsed_ms;
   if (kernel_ms) *kernel_ms = p->last_kernel_ms;
   if (launches) *launches = p->last_launches;
+  return GL3_OK;
+}
+
+extern "C" int gl3_time_attention(gl3_plan *p, int layer, int32_t position, int32_t n_reps, double *avg_ms) {
+  if (!p || !avg_ms) return fail(GL3_ERR_INVALID_ARGUMENT, "null argument");
+  if (layer < 0 || layer >= p->cfg.n_layers) return fail(GL3_ERR_INVALID_ARGUMENT, "layer %d out of range", layer);
+  if (position < 0 || position >= p->cfg.context_length)
+    return fail(GL3_ERR_INVALID_ARGUMENT, "position %d out of range [0,%d)", position, p->cfg.context_length);
+  if (n_reps < 1 || n_reps > 100000) return fail(GL3_ERR_INVALID_ARGUMENT, "n_reps %d", n_reps);
+  int rc = gl3_prepare(p);
+  if (rc) return rc;
+  set_state(p, 0, position);
+  HIP_TRY(hipMemcpyAsync(p->m.st, p->h_state, sizeof(DecodeState), hipMemcpyHostToDevice, p->stream));
+  HIP_TRY(launch_attention(p->m, layer, p->stream));  // warm-up
+  p->ev_used = 0;
+  for (int i = 0; i < n_reps; ++i) {
+    hipEvent_t e0 = next_event(p), e1 = next_event(p);
+    if (!e0 || !e1) return fail(GL3_ERR_DEVICE, "hipEventCreate failed");
+    HIP_TRY(hipEventRecord(e0, p->stream));
+    HIP_TRY(launch_attention(p->m, layer, p->stream));
+    HIP_TRY(hipEventRecord(e1, p->stream));
+  }
+  HIP_TRY(hipStreamSynchronize(p->stream));
+  double sum = 0;
+  for (int i = 0; i + 1 < p->ev_used; i += 2) {
+    float ms = 0;
+    HIP_TRY(hipEventElapsedTime(&ms, p->ev[i], p->ev[i + 1]));
+    sum += ms;
+  }
+  *avg_ms = sum / n_reps;
   return GL3_OK;
 }
 
@@ -1048,7 +1097,7 @@ extern "C" int gl3_op_attention(const float *q, const uint16_t *kcache, const ui
   int n_cu = 0;
   HIP_TRY(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev));
   ModelDev m{};
-  m.family = FAM_LLAMA;  // rotation at `pos` is the identity below (cos 1, sin 0)
+  m.family = FAM_LLAMA;
   m.n_layers = 1;
   m.n_heads = n_heads;
   m.n_kv = n_kv_heads;
@@ -1060,14 +1109,12 @@ extern "C" int gl3_op_attention(const float *q, const uint16_t *kcache, const ui
   m.sqrt_hd = (float)std::sqrt((double)hd);
   int ms = n_cu / n_kv_heads;
   m.max_split = ms < 1 ? 1 : (ms > 256 ? 256 : ms);
-  DevBuf layers, kc, vc, rc_, rs_, qkv, att, part, ctr, st;
+  DevBuf layers, kc, vc, qkv, att, part, ctr, st;
   DEV_ALLOC(layers, sizeof(LayerDev));
   DEV_ALLOC(kc, (size_t)n_kv_heads * m.ctxp * hd * 2);
   DEV_ALLOC(vc, (size_t)n_kv_heads * m.ctxp * hd * 2);
   DevBuf vstage;
   DEV_ALLOC(vstage, (size_t)ctx * hd * 2);
-  DEV_ALLOC(rc_, (size_t)ctx * (hd / 2) * 4);
-  DEV_ALLOC(rs_, (size_t)ctx * (hd / 2) * 4);
   DEV_ALLOC(qkv, (size_t)(q_dim + 2 * kv_dim) * 4);
   DEV_ALLOC(att, (size_t)q_dim * 4);
   DEV_ALLOC(part, (size_t)n_heads * m.max_split * (hd + 4) * 4);
@@ -1085,9 +1132,6 @@ extern "C" int gl3_op_attention(const float *q, const uint16_t *kcache, const ui
                            nullptr));
     HIP_TRY(hipDeviceSynchronize());
   }
-  std::vector<float> cosv((size_t)ctx * (hd / 2), 1.0f), sinv((size_t)ctx * (hd / 2), 0.0f);
-  HIP_TRY(hipMemcpy(rc_.ptr, cosv.data(), cosv.size() * 4, hipMemcpyHostToDevice));
-  HIP_TRY(hipMemcpy(rs_.ptr, sinv.data(), sinv.size() * 4, hipMemcpyHostToDevice));
   // qkv = [q, k(pos), v(pos)]: the kernel re-appends row pos of the cache unchanged
   std::vector<float> hq((size_t)q_dim + 2 * kv_dim);
   memcpy(hq.data(), q, (size_t)q_dim * 4);
@@ -1107,8 +1151,8 @@ extern "C" int gl3_op_attention(const float *q, const uint16_t *kcache, const ui
   m.layers = (const LayerDev *)layers.ptr;
   m.kc = (uint16_t *)kc.ptr;
   m.vc = (uint16_t *)vc.ptr;
-  m.rope_cos = (const float *)rc_.ptr;
-  m.rope_sin = (const float *)rs_.ptr;
+  m.rope_cos = nullptr;  // q is already rotated: no RoPE tables, q and k used as given
+  m.rope_sin = nullptr;
   m.qkv = (float *)qkv.ptr;
   m.att = (float *)att.ptr;
   m.part = (float *)part.ptr;

@@ -76,6 +76,7 @@ SIGNATURES = {
     "gl3_get_timing": (_I, [_P, _DP, _DP, _IP]),
     "gl3_get_phase_trace": (_I, [_P, _DP, ctypes.c_int32, _IP]),
     "gl3_get_phase_stamps": (_I, [_P, ctypes.POINTER(ctypes.c_uint64), ctypes.c_int64, _IP, _IP]),
+    "gl3_time_attention": (_I, [_P, _I, ctypes.c_int32, ctypes.c_int32, _DP]),
     "gl3_gguf_config": (_I, [ctypes.c_char_p, ctypes.c_int32, ctypes.c_uint32, ctypes.POINTER(Gl3Config)]),
     "gl3_create_from_gguf": (_I, [ctypes.c_char_p, ctypes.c_int32, ctypes.c_uint32, ctypes.POINTER(_P)]),
     "gl3_destroy": (None, [_P]),

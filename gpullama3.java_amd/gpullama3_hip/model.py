@@ -163,15 +163,58 @@ def q8_0_unpack(blocks, n):
     return q, scales
 
 
+PAR_CHUNK = 1 << 22  # elements per independently seeded chunk of a large tensor
+
+
+def _fill_chunk(spec, seed, out, i0, m, std):
+    """Elements [i0, i0 + m) of a large linear weight, from the chunk's own SFC64
+    stream (an order of magnitude faster than PCG64 here).  Q8_0 quants are raw
+    random bytes as int8 with every -128 redrawn uniformly from [-127, 127], which
+    is exactly U[-127, 127]."""
+    h = hashlib.sha256(f"{seed}:{spec.name}#{i0 // PAR_CHUNK}".encode()).digest()
+    bg = np.random.SFC64(int.from_bytes(h[:8], "little"))
+    rng = np.random.Generator(bg)
+    if spec.ggml_type == F16:
+        out[i0:i0 + m] = rng.standard_normal(m, dtype=np.float32) * np.float32(std)
+        return
+    b0, nb = i0 // 32, m // 32
+    sc = (np.abs(rng.standard_normal(nb, dtype=np.float32)) * np.float32(std / 127.0)).astype(np.float16)
+    out[b0:b0 + nb, :2] = sc.view(np.uint8).reshape(nb, 2)
+    q = bg.random_raw(m // 8).view(np.int8)
+    bad = np.flatnonzero(q == -128)
+    q[bad] = rng.integers(-127, 128, size=bad.size, dtype=np.int8)
+    out[b0:b0 + nb, 2:] = q.view(np.uint8).reshape(nb, 32)
+
+
+def _synth_large(spec, seed, std):
+    """Tensors above PAR_CHUNK elements: chunks of PAR_CHUNK elements, each from its
+    own seeded stream, generated on a thread pool (the generators release the GIL),
+    so an 8B-parameter model takes seconds instead of minutes.  Same distributions
+    as the single-stream path."""
+    import concurrent.futures as cf
+    import os
+    n = spec.n
+    out = np.empty(n, dtype=np.float16) if spec.ggml_type == F16 else np.empty((n // 32, 34), dtype=np.uint8)
+    starts = range(0, n, PAR_CHUNK)
+    workers = min(16, os.cpu_count() or 1)
+    with cf.ThreadPoolExecutor(workers) as ex:
+        list(ex.map(lambda i0: _fill_chunk(spec, seed, out, i0, min(PAR_CHUNK, n - i0), std), starts))
+    return out.view(np.uint8).reshape(-1)
+
+
 def synth_tensor(spec: TensorSpec, seed: int, norm_init="ones", std=0.02):
     """Seeded synthetic tensor in GGUF encoding.
 
     Linear weights: F16 ~ N(0, std); Q8_0 quants ~ U[-127, 127] with scales
     fp16(|N(0, std)| / 127).  Norm weights: 1.0 ("ones") or 1 + 0.1 N(0,1)
     ("random", used by the parity tests so a dropped norm weight is visible).
+    Linear weights of more than PAR_CHUNK elements come from per-chunk streams
+    (_synth_large).
     """
-    rng = _rng(seed, spec.name)
     n = spec.n
+    if spec.ggml_type != F32 and n > PAR_CHUNK:
+        return _synth_large(spec, seed, std)
+    rng = _rng(seed, spec.name)
     if spec.ggml_type == F32:
         if norm_init == "ones":
             v = np.ones(n, dtype=np.float32)

@@ -123,6 +123,13 @@ class HipMasterPlan:
         _ok(self.lib.gl3_get_timing(self.h, ctypes.byref(e), ctypes.byref(k), ctypes.byref(n)))
         return e.value, k.value, n.value
 
+    def time_attention(self, layer, position, n_reps=20):
+        """Average ms of the standalone attention kernel at `position` (gl3_time_attention;
+        overwrites the cache row at `position`)."""
+        ms = ctypes.c_double()
+        _ok(self.lib.gl3_time_attention(self.h, layer, position, n_reps, ctypes.byref(ms)))
+        return ms.value
+
     def phase_trace(self):
         """Per-phase durations (us) of the last persistent-kernel step (needs FLAG_PHASE_TRACE)."""
         out = np.zeros(16 + 10 * self.shape.n_layers, dtype=np.float64)

@@ -193,6 +193,14 @@ int gl3_get_phase_trace(gl3_plan *p, double *us_out, int32_t max_entries, int32_
  * start at i = 0).  Needs GL3_FLAG_PHASE_TRACE.  No reference counterpart. */
 int gl3_get_phase_stamps(gl3_plan *p, uint64_t *out, int64_t max_entries, int32_t *n_stamps, int32_t *n_workgroups);
 
+/* Measurement aid: runs the per-phase schedule's flash-decode attention kernel
+ * for `layer` at `position` n_reps times over the plan's KV cache, each launch
+ * bracketed by HIP events on the plan's stream, and returns the average launch
+ * duration in ms.  Each launch appends the plan's plain q/k/v vector as the
+ * cache row at `position` (the cache row is overwritten).  No reference
+ * counterpart (the reference times whole task graphs: llama-tornado:131-134). */
+int gl3_time_attention(gl3_plan *p, int layer, int32_t position, int32_t n_reps, double *avg_ms);
+
 /* The configuration of a GGUF model file, as the reference derives it: header
  * and metadata as GGUF.loadGGUFMetadata reads them (tensor/GGUF.java:43-92,
  * versions 2 and 3), the family from general.name as

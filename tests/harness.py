@@ -42,3 +42,15 @@ def prefill_kv(plan, ref, shape, npos, seed=3):
 def top2_margin(logits):
     s = np.sort(logits)
     return float(s[-1] - s[-2])
+
+
+def prefill_from_device(plan, ref, shape, npos, seed=3):
+    """The device's counter-based fp16 N(0,1) history (gl3_fill_kv_normal) for
+    positions [0, npos), read back (gl3_read_kv) into the oracle's fp32 cache:
+    both sides hold the same fp16-representable values.  Fast at long contexts."""
+    plan.fill_kv_normal(seed, npos)
+    for l in range(shape.n_layers):
+        k, v = plan.read_kv(l, 0, npos)
+        rk, rv = ref.kv(l)
+        rk[:npos] = k.view(np.float16)
+        rv[:npos] = v.view(np.float16)

@@ -6,6 +6,8 @@ row.  The weight totals below are computed independently from the model shapes
 (rows x cols per matrix); a dropped matrix, a wrong Q8_0 block size or a
 missing classifier changes them.
 """
+import pytest
+
 import bench
 from gpullama3_hip.model import CONFIGS, tensor_specs
 
@@ -52,8 +54,32 @@ def test_segments_fit_the_workloads():
     s = CONFIGS["llama1b_q8"]
     segs = bench.segments("llama1b_q8", 256, s.context_length)
     assert len(segs) == 8 and all(n == 32 for _, n in segs)
-    assert segs[0][0] == 0 and segs[-1][0] + 32 <= 2048
+    assert segs[0][0] == 0 and segs[-1][0] + 32 == 2048
     s8 = CONFIGS["llama8b_q8"]
     assert bench.segments("llama8b_q8", 384, s8.context_length) == [(8192, 128), (16384, 128), (32768, 128)]
     assert 32768 + 128 <= s8.context_length
     assert bench.segments("llama1b_q8", 64, s.context_length, [1024]) == [(1024, 64)]
+
+
+@pytest.mark.parametrize("steps", [1, 5, 20, 31, 32, 33, 64, 100, 255, 256, 257, 300, 1000])
+def test_segments_time_exactly_the_requested_steps(steps):
+    """--steps K times K tokens (no truncation); launches keep >= 32 tokens when K allows,
+    and the segments stay inside positions 0-2047 with their mean near the middle."""
+    s = CONFIGS["llama1b_q8"]
+    segs = bench.segments("llama1b_q8", steps, s.context_length)
+    assert sum(n for _, n in segs) == steps
+    assert all(n >= min(32, steps) for _, n in segs)
+    assert all(0 <= st and st + n <= 2048 for st, n in segs)
+    assert len(segs) == max(1, min(8, steps // 32))
+    if len(segs) == 1:
+        assert abs(segs[0][0] + steps / 2 - 1024) <= 1
+    for key, fills in (("llama8b_q8", bench.FILLS_8B),):
+        segs8 = bench.segments(key, steps, CONFIGS[key].context_length)
+        assert sum(n for _, n in segs8) == steps and [p for p, _ in segs8] == list(fills)
+
+
+def test_segments_reject_what_does_not_fit():
+    with pytest.raises(ValueError):
+        bench.segments("llama1b_q8", 0, 2304)
+    with pytest.raises(ValueError):
+        bench.segments("llama1b_q8", 2048, 2304)

@@ -8,20 +8,26 @@ exceeds that tolerance.  Both sides are teacher-forced with the oracle's tokens
 differently cannot make the sequences drift apart.
 
 * Llama-3.2-1B FP16, tied embeddings: 128-token random prompt, 128 greedy steps.
-* Llama-3.2-1B Q8_0 (untied Q8_0 classifier, FP16 embeddings): the same workload.
+* Llama-3.2-1B Q8_0 (untied Q8_0 classifier, FP16 embeddings): the same
+  workload, and 8 greedy steps from each start position of the benchmark's
+  segments across 0-2047 over an fp16 N(0,1) history.
 * Qwen3-0.6B Q8_0: 512-token prompt, 256 greedy steps (positions 0-767).
-* Phi-3-mini FP16 and Llama-3.1-8B Q8_0: a few steps at long contexts (4090 and
-  8192) over an fp16 N(0,1) history written into both caches.
+* Phi-3-mini FP16: 34 steps at positions 4062-4095 over an fp16 N(0,1) history.
+* Llama-3.1-8B Q8_0: 4 steps from each KV fill 8192, 16384 and 32768 over an
+  fp16 N(0,1) history (32 full-size layers; 16 and 32 attention splits of 1024
+  positions per kv head at the two longer fills).
 """
 import os
+import time
 
 import numpy as np
 import pytest
 
+import bench
 import oracle.oracle as orc
 from gpullama3_hip import HipMasterPlan
 from gpullama3_hip.model import CONFIGS, synth_model
-from harness import prefill_kv, top2_margin
+from harness import prefill_from_device, top2_margin
 
 pytestmark = pytest.mark.gpu
 
@@ -29,17 +35,11 @@ TOL = 2e-2
 THREADS = min(16, os.cpu_count() or 1)
 
 
-def run(shape, prompt, n_gen, start=0, seed=1234):
-    print(f"[case] {shape.name} prompt {len(prompt)} gen {n_gen} start {start}", flush=True)
-    tensors = synth_model(shape, seed, norm_init="ones")
-    plan = HipMasterPlan.initialize_plan(shape, tensors)
-    ref = orc.OracleModel(shape, tensors, kv_fp16=False, n_threads=THREADS)
-    if start:
-        prefill_kv(plan, ref, shape, start)
+def steps(plan, ref, prompt, n_gen, start):
+    """Teacher-forced steps from `start`; returns (worst |d|/std, greedy checks, near ties)."""
     worst, checked, ties = 0.0, 0, 0
     tok = int(prompt[0])
-    n = len(prompt) + n_gen
-    for i in range(n):
+    for i in range(len(prompt) + n_gen):
         pos = start + i
         lg, am = plan.forward(tok, pos)
         rl = ref.forward(tok, pos)
@@ -55,6 +55,17 @@ def run(shape, prompt, n_gen, start=0, seed=1234):
             else:
                 ties += 1
         tok = int(prompt[i + 1]) if i + 1 < len(prompt) else nxt
+    return worst, checked, ties
+
+
+def run(shape, prompt, n_gen, start=0, seed=1234):
+    print(f"[case] {shape.name} prompt {len(prompt)} gen {n_gen} start {start}", flush=True)
+    tensors = synth_model(shape, seed, norm_init="ones")
+    plan = HipMasterPlan.initialize_plan(shape, tensors)
+    ref = orc.OracleModel(shape, tensors, kv_fp16=False, n_threads=THREADS)
+    if start:
+        prefill_from_device(plan, ref, shape, start, seed=start)
+    worst, checked, ties = steps(plan, ref, prompt, n_gen, start)
     print(f"  max|d|/std {worst:.2e}; greedy ids equal at {checked} steps, {ties} within the tolerance", flush=True)
     plan.free_execution_plan()
     ref.close()
@@ -70,6 +81,29 @@ def test_llama1b_prompt_then_greedy(gpu, key):
     assert run(shape, prompt, 128) > 0
 
 
+def test_llama1b_q8_benchmark_segments(gpu):
+    """The benchmark's workload: 8 steps from each of its segment starts across
+    positions 0-2047 (KV history N(0,1) up to the start, as the benchmark fills it)."""
+    shape = CONFIGS["llama1b_q8"]
+    starts = [s for s, _ in bench.segments("llama1b_q8", 256, shape.context_length)]
+    assert len(starts) == 8 and starts[0] == 0 and starts[-1] + 32 == bench.SPAN_1B
+    print(f"[case] {shape.name} 8 steps at each start {starts}", flush=True)
+    tensors = synth_model(shape, 1234, norm_init="ones")
+    plan = HipMasterPlan.initialize_plan(shape, tensors)
+    ref = orc.OracleModel(shape, tensors, kv_fp16=False, n_threads=THREADS)
+    rng = np.random.default_rng(12)
+    total = 0
+    for s in starts:
+        if s:
+            prefill_from_device(plan, ref, shape, s, seed=1234 + s)
+        worst, checked, ties = steps(plan, ref, rng.integers(0, shape.vocab_size, 1), 7, s)
+        print(f"  start {s}: max|d|/std {worst:.2e}; greedy equal {checked}, ties {ties}", flush=True)
+        total += checked
+    assert total > 0
+    plan.free_execution_plan()
+    ref.close()
+
+
 def test_qwen3_prompt_then_greedy(gpu):
     shape = CONFIGS["qwen3_06b_q8"].with_(context_length=768)
     prompt = np.random.default_rng(8).integers(0, shape.vocab_size, 512)
@@ -79,10 +113,29 @@ def test_qwen3_prompt_then_greedy(gpu):
 def test_phi3_long_context(gpu):
     shape = CONFIGS["phi3_mini_f16"].with_(context_length=4096)
     prompt = np.random.default_rng(9).integers(0, shape.vocab_size, 2)
-    run(shape, prompt, 4, start=4090)
+    assert run(shape, prompt, 32, start=4062) > 0
 
 
-def test_llama8b_long_context(gpu):
-    shape = CONFIGS["llama8b_q8"].with_(context_length=8192 + 16)
-    prompt = np.random.default_rng(10).integers(0, shape.vocab_size, 2)
-    run(shape, prompt, 2, start=8192)
+def test_llama8b_kv_fills(gpu):
+    """Config 5: 4 steps from each fp16 N(0,1) KV fill (8192, 16384, 32768), one
+    plan and one oracle (fp32 KV, context 32768 + 16) for the three fills."""
+    shape = CONFIGS["llama8b_q8"].with_(context_length=32768 + 16)
+    print(f"[case] {shape.name} fills {bench.FILLS_8B}", flush=True)
+    t0 = time.perf_counter()
+    tensors = synth_model(shape, 1234, norm_init="ones")
+    plan = HipMasterPlan.initialize_plan(shape, tensors)
+    ref = orc.OracleModel(shape, tensors, kv_fp16=False, n_threads=THREADS)
+    print(f"  weights, plan and oracle: {time.perf_counter() - t0:.1f} s", flush=True)
+    rng = np.random.default_rng(10)
+    total = 0
+    for fill in bench.FILLS_8B:
+        t0 = time.perf_counter()
+        prefill_from_device(plan, ref, shape, fill, seed=1234 + fill)
+        t1 = time.perf_counter()
+        worst, checked, ties = steps(plan, ref, rng.integers(0, shape.vocab_size, 1), 3, fill)
+        print(f"  fill {fill}: max|d|/std {worst:.2e}; greedy equal {checked}, ties {ties} (prefill "
+              f"{t1 - t0:.1f} s, 4 steps {time.perf_counter() - t1:.1f} s)", flush=True)
+        total += checked
+    assert total > 0
+    plan.free_execution_plan()
+    ref.close()

@@ -109,13 +109,15 @@ def test_generate_greedy_across_launches(gpu):
     plan.free_execution_plan()
 
 
+@pytest.mark.parametrize("sched", sorted(SCHEDULES))
 @pytest.mark.parametrize("key", ["llama1b_q8", "llama8b_q8"])
-def test_upload_after_forward_replaces_ffn_weights(gpu, key):
+def test_upload_after_forward_replaces_ffn_weights(gpu, key, sched):
     """Weights uploaded after a forward are what the next forward uses, also
     where the persistent kernel keeps a rearranged copy of an FFN matrix (the
-    sliced Wdown of the fused FFN of the 1B Q8_0 shape)."""
+    sliced Wdown of the fused FFN of the 1B Q8_0 shape) and where the per-phase
+    schedule captured a graph."""
     shape = small(key)
-    plan, ref, tensors = build(shape)
+    plan, ref, tensors = build(shape, flags=SCHEDULES[sched])
     ref.close()
     plan.forward(5, 0)
     other = synth_model(shape, seed=99)
@@ -128,6 +130,83 @@ def test_upload_after_forward_replaces_ffn_weights(gpu, key):
         lg, am = plan.forward(t, p)
         rl = ref.forward(t, p)
         assert np.max(np.abs(lg - rl)) <= TOL_TIGHT * rl.std()
+    plan.free_execution_plan()
+    ref.close()
+
+
+@pytest.mark.parametrize("sched", sorted(SCHEDULES))
+def test_output_weight_uploaded_to_tied_plan(gpu, sched):
+    """A tied plan (no output.weight: the classifier is token_embd) that receives
+    an output.weight after its first forward uses it from then on, on both
+    schedules (the per-phase graph is captured again)."""
+    shape = small("llama1b_f16").with_(tied=True)
+    plan, ref, tensors = build(shape, flags=SCHEDULES[sched])
+    lg0, _ = plan.forward(5, 0)
+    assert np.max(np.abs(lg0 - ref.forward(5, 0))) <= TOL_TIGHT * lg0.std()
+    ref.close()
+    from gpullama3_hip.model import F16, TensorSpec, synth_tensor
+    spec = TensorSpec("output.weight", F16, shape.vocab_size, shape.dim)
+    tensors["output.weight"] = (spec, synth_tensor(spec, 99))
+    plan.upload("output.weight", F16, tensors["output.weight"][1])
+    plan.reset()
+    ref = orc.OracleModel(shape, tensors, kv_fp16=True)
+    for p, t in enumerate([5, 99, 7]):
+        lg, am = plan.forward(t, p)
+        rl = ref.forward(t, p)
+        assert np.max(np.abs(lg - rl)) <= TOL_TIGHT * rl.std(), p
+    plan.free_execution_plan()
+    ref.close()
+
+
+def test_plan_lifecycle_releases_device_memory(gpu):
+    """create / upload / forward / destroy returns every device allocation,
+    including the Q8_0 upload staging buffer (hipMemGetInfo before and after)."""
+    import ctypes
+    # the HIP runtime the library already loaded (not a second copy)
+    with open("/proc/self/maps") as f:
+        paths = sorted({ln.split()[-1] for ln in f if "libamdhip64.so" in ln})
+    assert paths, "libamdhip64 is not loaded"
+    hip = ctypes.CDLL(paths[0])
+    free, total = ctypes.c_size_t(), ctypes.c_size_t()
+
+    def free_bytes():
+        assert hip.hipDeviceSynchronize() == 0
+        assert hip.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
+        return free.value
+
+    # a 64k-row Q8_0 classifier: a 139 MB staging buffer per plan if it leaked
+    shape = small("llama1b_q8", vocab=65536)
+    tensors = synth_model(shape, 7, norm_init="random")
+
+    def cycle():
+        plan = HipMasterPlan.initialize_plan(shape, tensors)
+        plan.forward(3, 0)
+        plan.free_execution_plan()
+
+    cycle()  # runtime pools and code objects
+    f0 = free_bytes()
+    for _ in range(3):
+        cycle()
+    f1 = free_bytes()
+    print(f"device memory free before {f0 >> 20} MiB, after 3 cycles {f1 >> 20} MiB", flush=True)
+    assert f1 >= f0 - (32 << 20)
+
+
+@pytest.mark.parametrize("sched", sorted(SCHEDULES))
+def test_gqa8_decode_matches_oracle(gpu, sched):
+    """GQA group 8 (32 query heads over 4 kv heads): no compiled persistent shape,
+    so both flags run the per-phase schedule; against the oracle over a history
+    longer than two attention splits."""
+    shape = small("llama1b_q8").with_(n_kv_heads=4)
+    print(f"[case] GQA 8 {sched} shape={shape}", flush=True)
+    plan, ref, _ = build(shape, flags=SCHEDULES[sched], kv_fp16=True)
+    prefill_kv(plan, ref, shape, 130)
+    rng = np.random.default_rng(21)
+    toks = rng.integers(0, shape.vocab_size, 4)
+    for lg, am, rl in run_steps(plan, ref, toks, np.arange(130, 134)):
+        assert np.max(np.abs(lg - rl)) <= TOL_TIGHT * rl.std()
+        if top2_margin(rl) > TOL_TIGHT * rl.std():
+            assert am == orc.argmax(rl)
     plan.free_execution_plan()
     ref.close()
 
@@ -204,13 +283,21 @@ def test_plan_from_gguf_matches_upload(gpu, tmp_path, key):
     write_gguf(path, shape, tensors)
     a = HipMasterPlan.initialize_plan(shape, tensors)
     b = HipMasterPlan.from_gguf(path, shape.context_length)
+    # the oracle with the device's exact fp16 decode: the tight bar compares the same arithmetic
+    ref = orc.OracleModel(shape, tensors, kv_fp16=True, f16_exact=True)
     assert b.shape.vocab_size == shape.vocab_size and b.shape.n_layers == shape.n_layers
     for pos, tok in enumerate([3, 1000, 77, 4095]):
         la, ta = a.forward(tok, pos)
         lb, tb = b.forward(tok, pos)
         assert np.array_equal(la, lb) and ta == tb, pos
+        # the file-loaded plan against the oracle fed the tensors the file was written from
+        rl = ref.forward(tok, pos)
+        assert np.max(np.abs(lb - rl)) <= TOL_TIGHT * rl.std(), pos
+        if top2_margin(rl) > TOL_TIGHT * rl.std():
+            assert tb == orc.argmax(rl)
     a.free_execution_plan()
     b.free_execution_plan()
+    ref.close()
 
 
 @pytest.mark.parametrize("sched", sorted(SCHEDULES))

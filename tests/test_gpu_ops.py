@@ -80,10 +80,9 @@ def test_gemv_rejects_unsupported_width(gpu):
         P.op_gemv(Q8_0, w, 4, 1056, np.zeros(1056, np.float32))
 
 
-@pytest.mark.parametrize("hd,n_heads,n_kv", [(64, 32, 8), (128, 16, 8), (96, 32, 32), (128, 32, 8), (64, 8, 8)])
-@pytest.mark.parametrize("pos", [0, 1, 63, 64, 200, 1500, 4095])
-def test_attention_vs_oracle(gpu, hd, n_heads, n_kv, pos):
-    rng = np.random.default_rng(hd * 7919 + pos)
+def check_attention(hd, n_heads, n_kv, pos, seed):
+    print(f"[case] attention hd={hd} heads={n_heads} kv_heads={n_kv} pos={pos}", flush=True)
+    rng = np.random.Generator(np.random.SFC64(seed))
     kv_dim = n_kv * hd
     kc = rng.standard_normal((pos + 1, kv_dim), dtype=np.float32).astype(np.float16)
     vc = rng.standard_normal((pos + 1, kv_dim), dtype=np.float32).astype(np.float16)
@@ -95,6 +94,22 @@ def test_attention_vs_oracle(gpu, hd, n_heads, n_kv, pos):
         kvh = h // G
         ref = orc.attention_head(q[h * hd:(h + 1) * hd], kf, vf, kv_dim, hd, pos, offset=kvh * hd)
         assert np.max(np.abs(got[h * hd:(h + 1) * hd] - ref)) <= 2e-5 * np.abs(vc).max().astype(np.float32), h
+
+
+# (head_dim, query heads, kv heads): GQA groups 4, 2, 1 (MHA), 4 and 8
+@pytest.mark.parametrize("hd,n_heads,n_kv", [(64, 32, 8), (128, 16, 8), (96, 32, 32), (128, 32, 8), (64, 8, 8),
+                                             (128, 32, 4), (64, 32, 4)])
+@pytest.mark.parametrize("pos", [0, 1, 63, 64, 200, 1500, 4095])
+def test_attention_vs_oracle(gpu, hd, n_heads, n_kv, pos):
+    check_attention(hd, n_heads, n_kv, pos, hd * 7919 + pos + 31 * n_kv)
+
+
+# the Llama-3.1-8B attention shape (hd 128, GQA 4) and GQA 8 at the 16k and 32k KV fills:
+# 16 and 32 splits of 1024 positions per kv head, merged by log-sum-exp
+@pytest.mark.parametrize("hd,n_heads,n_kv", [(128, 32, 8), (128, 32, 4)])
+@pytest.mark.parametrize("pos", [16383, 32767])
+def test_attention_long_context_vs_oracle(gpu, hd, n_heads, n_kv, pos):
+    check_attention(hd, n_heads, n_kv, pos, pos + n_kv)
 
 
 def test_attention_one_position_is_exact(gpu):
