@@ -86,6 +86,7 @@ SIGNATURES = {
     "gl3_op_f16_to_f32": (_I, [_U16P, _SZ, _FP]),
     "gl3_op_gemv": (_I, [_I, _P, _I, _I, _FP, _FP, ctypes.c_float, _I, _FP]),
     "gl3_op_attention": (_I, [_FP, _U16P, _U16P, _I, _I, _I, _I, _FP]),
+    "gl3_op_attention_noalloc": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
 }
 
 _lib = None

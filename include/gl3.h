@@ -259,6 +259,31 @@ int gl3_op_gemv(int ggml_type, const void *w, int rows, int cols, const float *x
 int gl3_op_attention(const float *q, const uint16_t *kcache, const uint16_t *vcache, int n_heads,
                      int n_kv_heads, int head_dim, int pos, float *out);
 
+/* ---- Allocation-free entry point ---- */
+
+/* Scratch of gl3_op_attention_noalloc: one static device array of this many
+ * bytes per GPU, held until the process ends. */
+#define GL3_NOALLOC_SCRATCH_BYTES (1280u << 10)
+
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The computation of gl3_op_attention on device-resident
+ * buffers, in the plan's cache layout, appending the new row first:
+ *   qkv    device fp32 [n_heads*head_dim + 2*n_kv_heads*head_dim]: q (already
+ *          rotated), then the new k and v, which are written to the cache at pos;
+ *   kcache device fp16 K [n_kv_heads][ctxp][head_dim], rows < pos valid;
+ *   vcache device fp16 V in 16-position blocks [n_kv_heads][ctxp/16][head_dim][16];
+ *   out    device fp32 [n_heads*head_dim].
+ * ctxp is a multiple of 16 above pos.  The split partials, merge counters and
+ * control block live in the GPU's GL3_NOALLOC_SCRATCH_BYTES array (counters
+ * cleared by a kernel on every call); n_kv_heads <= 64, and a shape whose
+ * partials do not fit is rejected with GL3_ERR_INVALID_ARGUMENT.  Calls no
+ * allocating routine.  Enqueues on `stream` (a hipStream_t, NULL = default)
+ * and returns without waiting; calls that overlap on one GPU share its array
+ * and race. */
+int gl3_op_attention_noalloc(const float *qkv, uint16_t *kcache, uint16_t *vcache, int n_heads, int n_kv_heads,
+                             int head_dim, int ctxp, int pos, float *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif
