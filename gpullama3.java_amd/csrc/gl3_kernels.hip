@@ -284,6 +284,13 @@ __global__ __launch_bounds__(GL3_STEP_BLOCK, 1) void decode_step_kernel(ModelDev
       tk += 2;
       trace(m, tk++);
       SH::WO::prefetch(ld_mat(&L->wo), SH::dim, blk, nblk);
+      {
+        // workgroups without an attention item wait quietly for the attention output
+        const int msplit = max(1, min(min(m.max_split, 64), nblk / m.n_kv));
+        const int S = att_split_len(si.pos + 1, msplit, 16 * (SH::BS / GL3_WAVE));
+        if (blk >= m.n_kv * ((si.pos + S) / S))
+          quiet_wait(m.tatt, SH::gqa * SH::hd, SH::gqa * SH::hd - 1, m.n_kv, t_att, tw);
+      }
       SH::WO::run(ld_mat(&L->wo), SH::dim, InTag{m.tatt, t_att, tw}, nullptr, m.eps, OutTag{m.txb, t_wo, m.txa, t_x, tw},
                   nullptr, blk, nblk, lds, true);
       trace(m, tk++);

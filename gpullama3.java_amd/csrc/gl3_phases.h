@@ -881,6 +881,46 @@ struct GemvPhase {
   }
 };
 
+// Quiet wait of a workgroup that reaches a phase long before its input: wave 0
+// polls one cell per producer (cells base[i * stride + last], i < count <= 256:
+// each producer's last store), with long sleeps between rounds, until all
+// carry the tag; the phase's staging then reads the whole input as usual (and
+// still checks every cell).  Keeps waiting workgroups from polling the whole
+// vector for microseconds while the fabric carries other traffic: measured
+// +2.8% tokens/s on the Llama-3.2-1B Q8_0 shape for the workgroups without an
+// attention item.  Only for waits off the critical path: before the reduce of
+// the fused FFN (every workgroup waits there for the slowest) it cost 5%.
+__device__ __forceinline__ void quiet_wait(const uint2 *base, int stride, int last, int count, unsigned tag,
+                                           const TagWait &tw) {
+  if (threadIdx.x < GL3_WAVE) {
+    const int lane = threadIdx.x;
+    int e[4];
+    bool act[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = lane + j * GL3_WAVE;
+      act[j] = i < count;
+      e[j] = (act[j] ? i : 0) * stride + last;
+    }
+    unsigned spins = 0;
+    for (;;) {
+      bool ok = true;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (act[j]) {
+          const unsigned long long w = ld_coherent_u64((const unsigned long long *)(base + e[j]));
+          if ((unsigned)(w >> 32) == tag) act[j] = false;
+          else ok = false;
+        }
+      if (__all(ok)) break;
+      ++spins;
+      if (spins > tw.spin_limit || ld_coherent_u32(tw.err) != 0u) break;  // the staging wait reports it
+      __builtin_amdgcn_s_sleep(8);
+    }
+  }
+  __syncthreads();
+}
+
 // ------------------------------------------------- fused FFN (down slices)
 // When every workgroup owns 32 consecutive SwiGLU rows (one Q8_0 block of the
 // down projection's K), it multiplies them by its 32-column slice of Wdown
