@@ -301,6 +301,23 @@ def reference_workload(plan, shape, seed):
             "note": "(prompt + generated) / wall time from position 0, as the reference counts its tok/s"}
 
 
+def reference_workload_sampled(plan, shape, seed, temperature=0.1, topp=0.95):
+    """The same workload with the reference's default sampler (temperature 0.1,
+    top-p 0.95: Options.java:54-55), sampled on the device (gl3_generate_sampled)
+    with seeded draws in place of rng.nextFloat(1f)."""
+    plan.reset()
+    prompt = np.random.default_rng(seed).integers(0, shape.vocab_size, 128)
+    coins = np.random.default_rng(seed + 1).random(128).astype(np.float32)
+    plan.generate_sampled(prompt, 0, 4, temperature, topp, coins)  # warm the path
+    plan.reset()
+    t1 = time.perf_counter()
+    plan.generate_sampled(prompt, 0, 128, temperature, topp, coins)
+    t2 = time.perf_counter()
+    return {"prompt_tokens": 128, "generated_tokens": 128, "temperature": temperature, "topp": topp,
+            "tok_s": round(256 / (t2 - t1), 2), "wall_ms": round(1e3 * (t2 - t1), 3),
+            "note": "on-device top-p sampling, one launch per generated token plus the sampler"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -344,6 +361,8 @@ def main():
     if args.schedule == "persistent" and shape.context_length >= 256:
         ref_wl = reference_workload(plan, shape, args.seed)
         log(f"reference workload (128 prompt + 128 greedy from position 0): {ref_wl['tok_s']} tok/s")
+        ref_wl["sampled"] = reference_workload_sampled(plan, shape, args.seed)
+        log(f"reference workload with the default top-p sampler: {ref_wl['sampled']['tok_s']} tok/s")
     plan.free_execution_plan()
     cpu = None
     if not args.no_cpu_baseline:

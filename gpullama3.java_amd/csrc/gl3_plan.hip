@@ -108,6 +108,8 @@ struct gl3_plan {
   // staging
   uint8_t *staging = nullptr;
   size_t staging_bytes = 0;
+  float *probs = nullptr;             // sampler scratch [vocab]
+  float *coins = nullptr;             // sampler draws of the current generate call [context length]
   DecodeState *h_state = nullptr;     // pinned
   unsigned long long *h_best = nullptr;  // pinned [nbest]
   unsigned *h_err = nullptr;          // pinned
@@ -365,6 +367,8 @@ extern "C" int gl3_create(const gl3_config *cfg, gl3_plan **out) {
   TRY(dev_alloc(p, &m.best, 2 * (size_t)p->nbest));
   TRY(dev_alloc(p, &m.st, 1));
   TRY(dev_alloc(p, &m.tokens_out, (size_t)cfg->context_length));
+  TRY(dev_alloc(p, &p->probs, (size_t)cfg->vocab_size));
+  TRY(dev_alloc(p, &p->coins, (size_t)cfg->context_length));
   {
     int *pr = nullptr;
     TRY(dev_alloc(p, &pr, (size_t)cfg->context_length));
@@ -743,12 +747,18 @@ static hipEvent_t next_event(gl3_plan *p) {
 
 #define GL3_STEPS_PER_LAUNCH 256
 
-static int run_steps(gl3_plan *p, int n_steps) {
-  const bool timing = (p->cfg.flags & GL3_FLAG_TIMING) != 0;
+// Uploads the control block and starts the call's timing.
+static int begin_steps(gl3_plan *p) {
   p->ev_used = 0;
   p->last_launches = 0;
   HIP_TRY(hipMemcpyAsync(p->m.st, p->h_state, sizeof(DecodeState), hipMemcpyHostToDevice, p->stream));
   HIP_TRY(hipEventRecord(p->ev_begin, p->stream));
+  return GL3_OK;
+}
+
+// n_steps decode steps from the device control block as it stands.
+static int launch_steps(gl3_plan *p, int n_steps) {
+  const bool timing = (p->cfg.flags & GL3_FLAG_TIMING) != 0;
   // persistent kernel: up to GL3_STEPS_PER_LAUNCH steps per launch (grid
   // barriers between steps); graph schedule: one replay per step
   for (int i = 0; i < n_steps;) {
@@ -772,8 +782,19 @@ static int run_steps(gl3_plan *p, int n_steps) {
     ++p->last_launches;
     i += n;
   }
+  return GL3_OK;
+}
+
+static int end_steps(gl3_plan *p) {
   HIP_TRY(hipEventRecord(p->ev_end, p->stream));
   return GL3_OK;
+}
+
+static int run_steps(gl3_plan *p, int n_steps) {
+  int rc = begin_steps(p);
+  if (!rc) rc = launch_steps(p, n_steps);
+  if (!rc) rc = end_steps(p);
+  return rc;
 }
 
 static int finish_timing_and_errors(gl3_plan *p) {
@@ -858,6 +879,45 @@ extern "C" int gl3_generate_from_prompt(gl3_plan *p, const int32_t *prompt, int3
   // the argmax after step s is recorded at tokens_out[s]; the generated ones follow the last prompt step
   HIP_TRY(hipMemcpyAsync(tokens_out, p->m.tokens_out + (n_prompt - 1), (size_t)n_gen * 4, hipMemcpyDeviceToHost,
                          p->stream));
+  return finish_timing_and_errors(p);
+}
+
+extern "C" int gl3_generate_sampled(gl3_plan *p, const int32_t *prompt, int32_t n_prompt, int32_t position,
+                                    int32_t n_gen, float temperature, float topp, const float *coins,
+                                    int32_t *tokens_out) {
+  if (!p || !prompt || !coins || !tokens_out) return fail(GL3_ERR_INVALID_ARGUMENT, "null argument");
+  if (n_prompt <= 0 || n_gen <= 0) return fail(GL3_ERR_INVALID_ARGUMENT, "n_prompt %d and n_gen %d must be positive", n_prompt, n_gen);
+  if (!(temperature >= 0.0f) || std::isinf(temperature) || std::isnan(topp))
+    return fail(GL3_ERR_INVALID_ARGUMENT, "temperature %g / topp %g", (double)temperature, (double)topp);
+  if (p->cfg.vocab_size < 2) return fail(GL3_ERR_INVALID_ARGUMENT, "sampling needs a vocabulary of two or more");
+  const int64_t steps = (int64_t)n_prompt + n_gen - 1;
+  if (position < 0 || (int64_t)position + steps > p->cfg.context_length)
+    return fail(GL3_ERR_INVALID_ARGUMENT, "positions [%d, %lld) exceed context %d", position,
+                (long long)(position + steps), p->cfg.context_length);
+  for (int i = 0; i < n_prompt; ++i)
+    if (prompt[i] < 0 || prompt[i] >= p->cfg.vocab_size)
+      return fail(GL3_ERR_INVALID_ARGUMENT, "prompt token %d (index %d) out of range", prompt[i], i);
+  for (int i = 0; i < n_gen; ++i)
+    if (!(coins[i] >= 0.0f && coins[i] < 1.0f))
+      return fail(GL3_ERR_INVALID_ARGUMENT, "draw %d = %g is not in [0, 1)", i, (double)coins[i]);
+  int rc = gl3_prepare(p);
+  if (rc) return rc;
+  HIP_TRY(hipMemcpyAsync((void *)p->m.prompt, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, p->stream));
+  HIP_TRY(hipMemcpyAsync(p->coins, coins, (size_t)n_gen * 4, hipMemcpyHostToDevice, p->stream));
+  set_state(p, prompt[0], position);
+  p->h_state->n_prompt = n_prompt;
+  if ((rc = begin_steps(p))) return rc;
+  // the prompt tokens but the last: their logits are not used
+  if (n_prompt > 1 && (rc = launch_steps(p, n_prompt - 1))) return rc;
+  // then one step per generated token, each followed by the sampler, which
+  // makes the next step forward its token (no host round trip)
+  for (int k = 0; k < n_gen; ++k) {
+    if ((rc = launch_steps(p, 1))) return rc;
+    HIP_TRY(launch_sample(p->m.logits, p->cfg.vocab_size, temperature, topp, p->coins, k, p->probs, nullptr, p->m.st,
+                          p->m.tokens_out, p->stream));
+  }
+  if ((rc = end_steps(p))) return rc;
+  HIP_TRY(hipMemcpyAsync(tokens_out, p->m.tokens_out, (size_t)n_gen * 4, hipMemcpyDeviceToHost, p->stream));
   return finish_timing_and_errors(p);
 }
 
@@ -1081,6 +1141,29 @@ extern "C" int gl3_op_gemv(int ggml_type, const void *w, int rows, int cols, con
   HIP_TRY(launch_gemv(fmt, kmode, W, out_rows, (const float *)dx.ptr, norm_w ? (const float *)dn.ptr : nullptr, eps,
                       (float *)dy.ptr, nullptr, 0, nullptr));
   HIP_TRY(hipMemcpy(y, dy.ptr, (size_t)out_rows * 4, hipMemcpyDeviceToHost));
+  return GL3_OK;
+}
+
+extern "C" int gl3_op_sample(const float *logits, int32_t n, float temperature, float topp, const float *coins,
+                             int32_t n_draws, int32_t *tokens_out) {
+  if (!logits || !coins || !tokens_out || n < 2 || n_draws <= 0)
+    return fail(GL3_ERR_INVALID_ARGUMENT, "bad sample arguments (n %d, draws %d)", n, n_draws);
+  if (!(temperature >= 0.0f) || std::isinf(temperature) || std::isnan(topp))
+    return fail(GL3_ERR_INVALID_ARGUMENT, "temperature %g / topp %g", (double)temperature, (double)topp);
+  for (int i = 0; i < n_draws; ++i)
+    if (!(coins[i] >= 0.0f && coins[i] < 1.0f))
+      return fail(GL3_ERR_INVALID_ARGUMENT, "draw %d = %g is not in [0, 1)", i, (double)coins[i]);
+  DevBuf dl, dp, dc, dt;
+  DEV_ALLOC(dl, (size_t)n * 4);
+  DEV_ALLOC(dp, (size_t)n * 4);
+  DEV_ALLOC(dc, (size_t)n_draws * 4);
+  DEV_ALLOC(dt, (size_t)n_draws * 4);
+  HIP_TRY(hipMemcpy(dl.ptr, logits, (size_t)n * 4, hipMemcpyHostToDevice));
+  HIP_TRY(hipMemcpy(dc.ptr, coins, (size_t)n_draws * 4, hipMemcpyHostToDevice));
+  for (int k = 0; k < n_draws; ++k)
+    HIP_TRY(launch_sample((const float *)dl.ptr, n, temperature, topp, (const float *)dc.ptr, k, (float *)dp.ptr,
+                          nullptr, nullptr, (int *)dt.ptr, nullptr));
+  HIP_TRY(hipMemcpy(tokens_out, dt.ptr, (size_t)n_draws * 4, hipMemcpyDeviceToHost));
   return GL3_OK;
 }
 

@@ -69,6 +69,8 @@ SIGNATURES = {
     "gl3_forward": (_I, [_P, ctypes.c_int32, ctypes.c_int32, _FP, _IP]),
     "gl3_generate_greedy": (_I, [_P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _IP]),
     "gl3_generate_from_prompt": (_I, [_P, _IP, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _IP]),
+    "gl3_generate_sampled": (_I, [_P, _IP, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_float,
+                                 ctypes.c_float, _FP, _IP]),
     "gl3_reset": (_I, [_P]),
     "gl3_write_kv": (_I, [_P, _I, _I, _I, _U16P, _U16P]),
     "gl3_read_kv": (_I, [_P, _I, _I, _I, _U16P, _U16P]),
@@ -85,6 +87,7 @@ SIGNATURES = {
     "gl3_op_dequant_q8_0": (_I, [_P, _SZ, _FP]),
     "gl3_op_f16_to_f32": (_I, [_U16P, _SZ, _FP]),
     "gl3_op_gemv": (_I, [_I, _P, _I, _I, _FP, _FP, ctypes.c_float, _I, _FP]),
+    "gl3_op_sample": (_I, [_FP, ctypes.c_int32, ctypes.c_float, ctypes.c_float, _FP, ctypes.c_int32, _IP]),
     "gl3_op_attention": (_I, [_FP, _U16P, _U16P, _I, _I, _I, _I, _FP]),
     "gl3_op_attention_noalloc": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
 }

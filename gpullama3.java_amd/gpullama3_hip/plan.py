@@ -116,6 +116,18 @@ class HipMasterPlan:
         _ok(self.lib.gl3_generate_from_prompt(self.h, L.iptr(pr), pr.size, position, n_gen, L.iptr(out)))
         return out
 
+    def generate_sampled(self, prompt, position, n_gen, temperature, topp, coins):
+        """The prompt forwarded on the device, then n_gen tokens sampled on the device
+        (gl3_generate_sampled); coins[k] in [0, 1) is the draw of generated token k."""
+        pr = np.ascontiguousarray(prompt, dtype=np.int32)
+        c = np.ascontiguousarray(coins, dtype=np.float32)
+        if c.size < n_gen:
+            raise ValueError(f"{c.size} draws for {n_gen} tokens")
+        out = np.zeros(n_gen, dtype=np.int32)
+        _ok(self.lib.gl3_generate_sampled(self.h, L.iptr(pr), pr.size, position, n_gen, float(temperature),
+                                          float(topp), L.fptr(c), L.iptr(out)))
+        return out
+
     def timing(self):
         e = ctypes.c_double()
         k = ctypes.c_double()
@@ -230,6 +242,15 @@ def op_gemv(ggml_type, w, rows, cols, x, norm_w=None, eps=1e-5, mode=L.GEMV_STOR
     nw = None if norm_w is None else np.ascontiguousarray(norm_w, dtype=np.float32)
     _ok(L.load().gl3_op_gemv(ggml_type, ctypes.c_void_p(wb.ctypes.data), rows, cols, L.fptr(x),
                              L.fptr(nw) if nw is not None else None, eps, mode, L.fptr(out)))
+    return out
+
+
+def op_sample(logits, temperature, topp, coins):
+    """Device sampler on host logits, one token per draw (gl3_op_sample)."""
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    c = np.ascontiguousarray(coins, dtype=np.float32)
+    out = np.zeros(c.size, dtype=np.int32)
+    _ok(L.load().gl3_op_sample(L.fptr(x), x.size, float(temperature), float(topp), L.fptr(c), c.size, L.iptr(out)))
     return out
 
 

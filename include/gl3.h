@@ -156,6 +156,22 @@ int gl3_generate_greedy(gl3_plan *p, int32_t token, int32_t position, int32_t n_
 int gl3_generate_from_prompt(gl3_plan *p, const int32_t *prompt, int32_t n_prompt, int32_t position, int32_t n_gen,
                              int32_t *tokens_out);
 
+/* The reference's generation loop with a sampling Sampler, entirely on the
+ * device (InferenceEngine.generateTokensGPULlama, inference/InferenceEngine.java:309-355,
+ * with Sampler.selectSampler, inference/sampler/Sampler.java:74-122): the
+ * n_prompt prompt tokens are forwarded from `position` (logits unused), then
+ * each of the n_gen tokens is sampled on the device from the last step's
+ * logits and forwarded: temperature 0 takes the first maximum (TENSOR_ARGMAX);
+ * otherwise the logits are divided by the temperature and turned into
+ * probabilities, then sampled by CategoricalSampler (CategoricalSampler.java:31-42)
+ * when topp <= 0 or topp >= 1, else by ToppSampler (ToppSampler.java:61-156).
+ * coins[k] in [0, 1) is the draw for generated token k (the reference's
+ * rng.nextFloat(1f)).  Cumulative sums are exact (fixed point) and the nucleus
+ * is visited in descending probability, ties by index.  tokens_out receives
+ * the n_gen tokens.  Requires position + n_prompt + n_gen - 1 <= context_length. */
+int gl3_generate_sampled(gl3_plan *p, const int32_t *prompt, int32_t n_prompt, int32_t position, int32_t n_gen,
+                         float temperature, float topp, const float *coins, int32_t *tokens_out);
+
 /* Zero the KV cache (a fresh State: inference/state/LlamaState.java:61-64). */
 int gl3_reset(gl3_plan *p);
 
@@ -251,6 +267,12 @@ int gl3_op_f16_to_f32(const uint16_t *in, size_t n, float *out);
  * kernels/TransformerComputeKernelsLayered.java:650-1057. */
 int gl3_op_gemv(int ggml_type, const void *w, int rows, int cols, const float *x, const float *norm_w,
                 float eps, int mode, float *y);
+
+/* The device sampler of gl3_generate_sampled on host logits [n] (n >= 2), once
+ * per draw: tokens_out[k] is the token sampled with coins[k]
+ * (Sampler.selectSampler, inference/sampler/Sampler.java:74-122). */
+int gl3_op_sample(const float *logits, int32_t n, float temperature, float topp, const float *coins, int32_t n_draws,
+                  int32_t *tokens_out);
 
 /* Decode attention of all heads at position pos over an fp16 cache [pos+1][n_kv][hd]
  * (rows for t <= pos): out[n_heads*hd].  q is [n_heads*hd] fp32, already rotated.

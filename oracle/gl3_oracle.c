@@ -301,6 +301,206 @@ void orc_softmax(float *x, int size) {
   for (int i = 0; i < size; ++i) x[i] = x[i] / sum;
 }
 
+/* ------------------------------------------------------------- sampling
+ * Sampler.selectSampler (inference/sampler/Sampler.java:74-122) applied to one
+ * logits vector: temperature 0 -> TENSOR_ARGMAX; otherwise the logits are
+ * divided by the temperature (FloatTensor.divideInPlace, FloatTensor.java:203-205),
+ * turned into probabilities (softmaxInPlace, :211-219) and handed to
+ * CategoricalSampler (CategoricalSampler.java:31-42) when topp <= 0 or topp >= 1,
+ * else to ToppSampler (ToppSampler.java:61-156).  `coin` is the value the
+ * reference draws with rng.nextFloat(1f). */
+
+/* ToppSampler.siftDown (ToppSampler.java:30-44) with the comparator of
+ * sampleFromFloatTensor (:60: comparingDouble(getFloat).reversed()): a node
+ * goes below a child with a strictly larger probability. */
+static void topp_sift_down(int *a, int from, int n, const float *p) {
+  int prev = from, next;
+  while ((next = 2 * prev + 1) < n) {
+    int r = 2 * prev + 2;
+    if (r < n && (double)p[a[r]] > (double)p[a[next]]) next = r;
+    if ((double)p[a[next]] > (double)p[a[prev]]) {
+      int t = a[prev];
+      a[prev] = a[next];
+      a[next] = t;
+      prev = next;
+    } else {
+      break;
+    }
+  }
+}
+
+/* probabilities descending, then index ascending */
+static const float *g_sort_p;
+static int cmp_desc(const void *x, const void *y) {
+  int a = *(const int *)x, b = *(const int *)y;
+  if (g_sort_p[a] > g_sort_p[b]) return -1;
+  if (g_sort_p[a] < g_sort_p[b]) return 1;
+  return a < b ? -1 : (a > b);
+}
+
+int orc_sample(const float *logits, int n, float temperature, float topp, float coin, float *probs, int *idx,
+               orc_sample_info *info) {
+  orc_sample_info dummy;
+  if (!info) info = &dummy;
+  info->token_exact = -1;
+  info->margin_exact = 0.0;
+  info->quirk = 0;
+  info->nucleus = 0;
+  info->ref_shift = 0.0;
+  if (temperature == 0.0f) {  /* Sampler.java:76-78 */
+    int t = orc_argmax(logits, n);
+    info->token_exact = t;
+    info->margin_exact = 1.0;
+    return t;
+  }
+  for (int i = 0; i < n; ++i) probs[i] = logits[i] / temperature;  /* FloatTensor.java:203-205 */
+  /* softmaxInPlace (FloatTensor.java:211-219), keeping the exponentials for the exact path */
+  float maxv = -INFINITY;
+  for (int i = 0; i < n; ++i) maxv = probs[i] > maxv ? probs[i] : maxv;
+  float *pe = (float *)malloc(sizeof(float) * (size_t)n);
+  float sum = 0.0f;
+  double sum_d = 0.0;
+  for (int i = 0; i < n; ++i) {
+    probs[i] = (float)exp((double)(probs[i] - maxv));
+    pe[i] = probs[i];
+    sum += probs[i];
+    sum_d += (double)probs[i];
+  }
+  for (int i = 0; i < n; ++i) probs[i] = probs[i] / sum;
+  /* exact normalisation: the exponentials over the float nearest their exact sum */
+  const float sum_f = (float)sum_d;
+  for (int i = 0; i < n; ++i) pe[i] = pe[i] / sum_f;
+  int token;
+  if (topp <= 0 || topp >= 1) {
+    /* CategoricalSampler.sampleFromFloatTensor (CategoricalSampler.java:31-42) */
+    float cdf = 0.0f;
+    token = n - 1;
+    for (int i = 0; i < n; ++i) {
+      cdf += probs[i];
+      if (coin < cdf) {
+        token = i;
+        break;
+      }
+    }
+    /* the walk over the exact probabilities in double: decision and distance from its boundaries */
+    double c = 0.0, prev = 0.0;
+    int te = n - 1, hit = 0;
+    for (int i = 0; i < n; ++i) {
+      prev = c;
+      c += (double)pe[i];
+      if ((double)coin < c) {
+        te = i;
+        hit = 1;
+        break;
+      }
+    }
+    info->token_exact = te;
+    if (hit) {
+      const double m1 = c - (double)coin, m2 = (double)coin - prev;
+      info->margin_exact = m1 < m2 ? m1 : m2;
+    }
+    double at_ref = 0.0;
+    for (int i = 0; i <= token; ++i) at_ref += (double)pe[i];
+    info->ref_shift = fabs((double)cdf - at_ref);
+    info->nucleus = n;
+    free(pe);
+    return token;
+  }
+  /* ToppSampler.sampleFromFloatTensor (ToppSampler.java:58-78): crop candidates below the cutoff */
+  int head = 0, tail = n - 1;
+  const float cutoff = (1.0f - topp) / (float)(n - 1);
+  for (int i = 0; i < n; ++i) {
+    if (probs[i] >= cutoff)
+      idx[head++] = i;
+    else
+      idx[tail--] = i;
+  }
+  const int n0 = head;
+  /* processTopP (ToppSampler.java:103-156): heap, extraction until the cumulative mass exceeds topp */
+  for (int i = n0 / 2 - 1; i >= 0; --i) topp_sift_down(idx, i, n0, probs);
+  float cum = 0.0f;
+  double cum_pe = 0.0;
+  int last = 0;
+  float prev_val = INFINITY;
+  for (int i = n0 - 1; i >= 0; i--) {
+    int t = idx[0];
+    idx[0] = idx[i];
+    idx[i] = t;
+    const float v = probs[idx[i]];
+    if (v > prev_val) info->quirk = 1;  /* extraction not in descending order (the siftDown bound below) */
+    prev_val = v;
+    cum += v;
+    cum_pe += (double)pe[idx[i]];
+    if (cum > topp) {
+      last = i;
+      break;
+    }
+    topp_sift_down(idx, 0, i - 1, probs);  /* ToppSampler.java:128: the bound is i - 1 */
+  }
+  const float r = coin * cum;
+  float cdf = 0.0f;
+  double cdf_pe = 0.0;
+  token = idx[last];
+  for (int i = n0 - 1; i >= last; i--) {
+    cdf += probs[idx[i]];
+    cdf_pe += (double)pe[idx[i]];
+    if (r < cdf) {
+      token = idx[i];
+      break;
+    }
+  }
+  {
+    const double s1 = fabs((double)cum - cum_pe), s2 = fabs((double)cdf - cdf_pe);
+    info->ref_shift = s1 > s2 ? s1 : s2;
+  }
+  /* exact semantics: the exact probabilities' candidates sorted (descending, ties by index),
+   * cumulative mass in double until it exceeds topp, r = coin * mass, walk */
+  int *ord = (int *)malloc(sizeof(int) * (size_t)(n > 0 ? n : 1));
+  int m = 0;
+  for (int i = 0; i < n; ++i)
+    if (pe[i] >= cutoff) ord[m++] = i;
+  g_sort_p = pe;
+  qsort(ord, (size_t)m, sizeof(int), cmp_desc);
+  double c = 0.0, before = 0.0;
+  int k = m, crossed = 0;
+  for (int i = 0; i < m; ++i) {
+    before = c;
+    c += (double)pe[ord[i]];
+    if (c > (double)topp) {
+      k = i + 1;
+      crossed = 1;
+      break;
+    }
+  }
+  double margin = crossed ? c - (double)topp : (double)topp - c;
+  if (crossed && k > 1) {  /* a smaller topp would have stopped one token earlier */
+    const double d = (double)topp - before;
+    margin = margin < d ? margin : d;
+  }
+  const double rr = (double)coin * c;
+  double w = 0.0, wprev = 0.0;
+  info->token_exact = m > 0 ? ord[k - 1] : n - 1;
+  int found = 0;
+  for (int i = 0; i < k; ++i) {
+    wprev = w;
+    w += (double)pe[ord[i]];
+    if (rr < w) {
+      info->token_exact = ord[i];
+      double d1 = w - rr, d2 = rr - wprev;
+      d1 = d1 < d2 ? d1 : d2;
+      margin = margin < d1 ? margin : d1;
+      found = 1;
+      break;
+    }
+  }
+  if (!found) margin = 0.0;  /* only rounding ends the walk without a pick */
+  info->margin_exact = margin;
+  info->nucleus = k;
+  free(ord);
+  free(pe);
+  return token;
+}
+
 /* FloatTensor.argmax (FloatTensor.java:138-151): first maximum wins. */
 int orc_argmax(const float *x, int size) {
   int mi = 0;

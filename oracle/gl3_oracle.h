@@ -94,6 +94,26 @@ void orc_rmsnorm(float *out, const float *x, const float *w, int offset, int siz
 void orc_rope_tables(int ctx, int head_size, double theta, float *cr, float *ci);
 void orc_softmax(float *x, int size);
 int orc_argmax(const float *x, int size);
+/* Sampler.selectSampler + CategoricalSampler / ToppSampler on one logits vector
+ * (inference/sampler/Sampler.java:74-122, CategoricalSampler.java:31-42,
+ * ToppSampler.java:61-156): returns the token the reference samples for the
+ * draw `coin` (rng.nextFloat(1f)).  probs and idx are n-element scratch.
+ * info (nullable) also gets the decision in exact arithmetic (the
+ * exponentials divided by the float nearest their exact sum, cumulative sums
+ * in double, candidates in descending order with ties by index), its distance
+ * from the nearest decision boundary, the nucleus size, whether the
+ * reference's heap extracted the nucleus out of descending order, and how far
+ * the reference's float sums at its decision are from the exact ones. */
+typedef struct {
+  int token_exact;
+  double margin_exact;
+  int quirk;
+  int nucleus;
+  double ref_shift;
+} orc_sample_info;
+int orc_sample(const float *logits, int n, float temperature, float topp, float coin, float *probs, int *idx,
+               orc_sample_info *info);
+
 /* attention for one head: q[hs], cache rows at k/v + t*kv_stride, t in [0,pos] */
 void orc_attention_head(const float *q, const float *kcache, const float *vcache, int kv_stride,
                         int head_size, int pos, float *att_scratch, float *out);

@@ -31,6 +31,11 @@ class OrcConfig(ctypes.Structure):
                 ("f16_exact", ctypes.c_int), ("n_threads", ctypes.c_int)]
 
 
+class SampleInfo(ctypes.Structure):
+    _fields_ = [("token_exact", ctypes.c_int), ("margin_exact", ctypes.c_double), ("quirk", ctypes.c_int),
+                ("nucleus", ctypes.c_int), ("ref_shift", ctypes.c_double)]
+
+
 _lib = None
 _FP = ctypes.POINTER(ctypes.c_float)
 
@@ -69,6 +74,7 @@ def load():
             "orc_softmax": (None, [_FP, I]),
             "orc_argmax": (I, [_FP, I]),
             "orc_attention_head": (None, [_FP, _FP, _FP, I, I, I, _FP, _FP]),
+            "orc_sample": (I, [_FP, I, F, F, F, _FP, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(SampleInfo)]),
             "orc_set_simd": (None, [I]),
         }
         for name, (res, args) in sig.items():
@@ -197,3 +203,19 @@ def softmax(x):
 def argmax(x):
     x = np.ascontiguousarray(x, dtype=np.float32)
     return load().orc_argmax(fp(x), x.size)
+
+
+def sample(logits, temperature, topp, coin):
+    """The reference's Sampler on one logits vector for the draw `coin`:
+    (token, exact token, exact margin, heap-order quirk, nucleus size); sample_info
+    also returns the reference's float-sum shift at its decision."""
+    lib = load()
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    n = x.size
+    probs = np.zeros(n, dtype=np.float32)
+    idx = np.zeros(n, dtype=np.int32)
+    info = SampleInfo()
+    tok = lib.orc_sample(fp(x), n, float(temperature), float(topp), float(coin), fp(probs),
+                         idx.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), ctypes.byref(info))
+    sample.last_shift = info.ref_shift
+    return tok, info.token_exact, info.margin_exact, info.quirk, info.nucleus
