@@ -45,4 +45,15 @@ hipError_t launch_kv_rows(uint16_t *kc, uint16_t *vc, uint16_t *rk, uint16_t *rv
                           int npos, bool to_cache, hipStream_t st);
 hipError_t launch_fill_normal_vt(uint16_t *vt, int hd, int npos, unsigned long long seed, hipStream_t st);
 
+// batched prefill (gl3_prefill.hip)
+bool prefill_supported(const ModelDev &m);
+hipError_t launch_prefill_gemm(int fmt, int mode, const Mat &W, int N, const _Float16 *Xh, const _Float16 *Xl, int T,
+                               float *Y, _Float16 *Yh, _Float16 *Yl, hipStream_t s);
+hipError_t launch_embed_rows(const ModelDev &m, const int *tokens, int T, float *X, hipStream_t s);
+hipError_t launch_rmsnorm_rows(const float *X, const float *w, float eps, int dim, int T, _Float16 *Yh, _Float16 *Yl,
+                               hipStream_t s);
+hipError_t launch_rope_kv_rows(const ModelDev &m, int layer, float *QKV, int p0, int T, hipStream_t s);
+hipError_t launch_attn_rows(const ModelDev &m, int layer, const float *QKV, int p0, int T, _Float16 *Oh, _Float16 *Ol,
+                            hipStream_t s);
+
 }  // namespace gl3

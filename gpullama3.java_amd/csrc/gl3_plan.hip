@@ -108,6 +108,11 @@ struct gl3_plan {
   // staging
   uint8_t *staging = nullptr;
   size_t staging_bytes = 0;
+  // batched prefill workspace, allocated on first use: residual rows, q/k/v
+  // rows, and two pairs of hi / lo fp16 activation planes (a: normed rows and
+  // attention output, b: SwiGLU output)
+  float *pf_x = nullptr, *pf_qkv = nullptr;
+  _Float16 *pf_ah = nullptr, *pf_al = nullptr, *pf_bh = nullptr, *pf_bl = nullptr;
   float *probs = nullptr;             // sampler scratch [vocab]
   float *coins = nullptr;             // sampler draws of the current generate call [context length]
   DecodeState *h_state = nullptr;     // pinned
@@ -858,6 +863,87 @@ extern "C" int gl3_generate_greedy(gl3_plan *p, int32_t token, int32_t position,
   return finish_timing_and_errors(p);
 }
 
+// ------------------------------------------------------------- prefill
+
+#define GL3_PREFILL_ROWS 512  // prompt rows per block of the batched prefill
+
+static bool use_prefill(const gl3_plan *p) {
+  return !(p->cfg.flags & GL3_FLAG_STEPWISE_PROMPT) && prefill_supported(p->m);
+}
+
+// Forwards the n tokens at d_tokens (device) at positions pos0 .. pos0 + n - 1
+// through every layer, GL3_PREFILL_ROWS rows at a time: fills their K and V and
+// nothing else (the reference's prompt loop, whose logits are unused).
+static int run_prefill(gl3_plan *p, const int *d_tokens, int n, int pos0) {
+  const ModelDev &m = p->m;
+  const int R = GL3_PREFILL_ROWS;
+  int rc;
+  if (!p->pf_x) {
+    const size_t wa = (size_t)R * std::max(m.dim, m.q_dim), wb = (size_t)R * m.hidden;
+    if ((rc = dev_alloc(p, &p->pf_x, (size_t)R * m.dim)) || (rc = dev_alloc(p, &p->pf_qkv, (size_t)R * (m.q_dim + 2 * m.kv_dim))) ||
+        (rc = dev_alloc(p, &p->pf_ah, wa)) || (rc = dev_alloc(p, &p->pf_al, wa)) ||
+        (rc = dev_alloc(p, &p->pf_bh, wb)) || (rc = dev_alloc(p, &p->pf_bl, wb)))
+      return rc;
+  }
+  hipStream_t s = p->stream;
+  _Float16 *ah = p->pf_ah, *al = p->pf_al, *bh = p->pf_bh, *bl = p->pf_bl;
+  for (int r0 = 0; r0 < n; r0 += R) {
+    const int T = std::min(R, n - r0), p0 = pos0 + r0;
+    HIP_TRY(launch_embed_rows(m, d_tokens + r0, T, p->pf_x, s));
+    for (int l = 0; l < m.n_layers; ++l) {
+      HIP_TRY(launch_rmsnorm_rows(p->pf_x, p->attn_norm[l], m.eps, m.dim, T, ah, al, s));
+      HIP_TRY(launch_prefill_gemm(m.fmt, MODE_STORE, p->qkv[l].view(), m.q_dim + 2 * m.kv_dim, ah, al, T, p->pf_qkv,
+                                  nullptr, nullptr, s));
+      HIP_TRY(launch_rope_kv_rows(m, l, p->pf_qkv, p0, T, s));
+      HIP_TRY(launch_attn_rows(m, l, p->pf_qkv, p0, T, ah, al, s));
+      HIP_TRY(launch_prefill_gemm(m.fmt, MODE_RESIDUAL, p->wo[l].view(), m.dim, ah, al, T, p->pf_x, nullptr, nullptr, s));
+      HIP_TRY(launch_rmsnorm_rows(p->pf_x, p->ffn_norm[l], m.eps, m.dim, T, ah, al, s));
+      HIP_TRY(launch_prefill_gemm(m.fmt, MODE_SWIGLU, p->gu[l].view(), m.hidden, ah, al, T, nullptr, bh, bl, s));
+      HIP_TRY(launch_prefill_gemm(m.fmt, MODE_RESIDUAL, p->down[l].view(), m.dim, bh, bl, T, p->pf_x, nullptr, nullptr, s));
+    }
+  }
+  return GL3_OK;
+}
+
+// The prompt but its last token: batched prefill where the shape allows it,
+// else decode steps; then the control block stands at the last prompt token
+// (step n_prompt - 1), whose forward produces the first generated token.
+static int run_prompt(gl3_plan *p, const int32_t *prompt, int n_prompt, int position) {
+  int rc;
+  if (n_prompt > 1 && use_prefill(p)) {
+    set_state(p, prompt[n_prompt - 1], position + n_prompt - 1);
+    p->h_state->step = n_prompt - 1;
+    p->h_state->n_prompt = n_prompt;
+    if ((rc = begin_steps(p))) return rc;
+    return run_prefill(p, p->m.prompt, n_prompt - 1, position);
+  }
+  set_state(p, prompt[0], position);
+  p->h_state->n_prompt = n_prompt;
+  if ((rc = begin_steps(p))) return rc;
+  return n_prompt > 1 ? launch_steps(p, n_prompt - 1) : GL3_OK;
+}
+
+extern "C" int gl3_prefill(gl3_plan *p, const int32_t *tokens, int32_t n, int32_t position) {
+  if (!p || !tokens) return fail(GL3_ERR_INVALID_ARGUMENT, "null argument");
+  if (n <= 0 || position < 0 || (int64_t)position + n > p->cfg.context_length)
+    return fail(GL3_ERR_INVALID_ARGUMENT, "positions [%d, %lld) exceed context %d", position, (long long)position + n,
+                p->cfg.context_length);
+  for (int i = 0; i < n; ++i)
+    if (tokens[i] < 0 || tokens[i] >= p->cfg.vocab_size)
+      return fail(GL3_ERR_INVALID_ARGUMENT, "token %d (index %d) out of range", tokens[i], i);
+  int rc = gl3_prepare(p);
+  if (rc) return rc;
+  if (!prefill_supported(p->m))
+    return fail(GL3_ERR_UNSUPPORTED, "batched prefill needs head_dim 64, 96 or 128 (head_dim %d)", p->cfg.head_dim);
+  HIP_TRY(hipMemcpyAsync((void *)p->m.prompt, tokens, (size_t)n * 4, hipMemcpyHostToDevice, p->stream));
+  p->ev_used = 0;
+  p->last_launches = 0;
+  HIP_TRY(hipEventRecord(p->ev_begin, p->stream));
+  if ((rc = run_prefill(p, p->m.prompt, n, position))) return rc;
+  if ((rc = end_steps(p))) return rc;
+  return finish_timing_and_errors(p);
+}
+
 extern "C" int gl3_generate_from_prompt(gl3_plan *p, const int32_t *prompt, int32_t n_prompt, int32_t position,
                                         int32_t n_gen, int32_t *tokens_out) {
   if (!p || !prompt || !tokens_out) return fail(GL3_ERR_INVALID_ARGUMENT, "null argument");
@@ -872,9 +958,9 @@ extern "C" int gl3_generate_from_prompt(gl3_plan *p, const int32_t *prompt, int3
   int rc = gl3_prepare(p);
   if (rc) return rc;
   HIP_TRY(hipMemcpyAsync((void *)p->m.prompt, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, p->stream));
-  set_state(p, prompt[0], position);
-  p->h_state->n_prompt = n_prompt;
-  if ((rc = run_steps(p, (int)steps))) return rc;
+  if ((rc = run_prompt(p, prompt, n_prompt, position))) return rc;
+  if ((rc = launch_steps(p, n_gen))) return rc;
+  if ((rc = end_steps(p))) return rc;
   HIP_TRY(launch_finish(p->m, p->stream));
   // the argmax after step s is recorded at tokens_out[s]; the generated ones follow the last prompt step
   HIP_TRY(hipMemcpyAsync(tokens_out, p->m.tokens_out + (n_prompt - 1), (size_t)n_gen * 4, hipMemcpyDeviceToHost,
@@ -904,11 +990,8 @@ extern "C" int gl3_generate_sampled(gl3_plan *p, const int32_t *prompt, int32_t 
   if (rc) return rc;
   HIP_TRY(hipMemcpyAsync((void *)p->m.prompt, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, p->stream));
   HIP_TRY(hipMemcpyAsync(p->coins, coins, (size_t)n_gen * 4, hipMemcpyHostToDevice, p->stream));
-  set_state(p, prompt[0], position);
-  p->h_state->n_prompt = n_prompt;
-  if ((rc = begin_steps(p))) return rc;
   // the prompt tokens but the last: their logits are not used
-  if (n_prompt > 1 && (rc = launch_steps(p, n_prompt - 1))) return rc;
+  if ((rc = run_prompt(p, prompt, n_prompt, position))) return rc;
   // then one step per generated token, each followed by the sampler, which
   // makes the next step forward its token (no host round trip)
   for (int k = 0; k < n_gen; ++k) {

@@ -29,6 +29,7 @@ TYPE_F32, TYPE_F16, TYPE_Q8_0 = 0, 1, 8
 FLAG_PHASE_KERNELS = 1
 FLAG_TIMING = 2
 FLAG_PHASE_TRACE = 4
+FLAG_STEPWISE_PROMPT = 8
 
 GEMV_STORE, GEMV_RESIDUAL, GEMV_SWIGLU = 0, 1, 2
 
@@ -68,6 +69,7 @@ SIGNATURES = {
     "gl3_prepare": (_I, [_P]),
     "gl3_forward": (_I, [_P, ctypes.c_int32, ctypes.c_int32, _FP, _IP]),
     "gl3_generate_greedy": (_I, [_P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _IP]),
+    "gl3_prefill": (_I, [_P, _IP, ctypes.c_int32, ctypes.c_int32]),
     "gl3_generate_from_prompt": (_I, [_P, _IP, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _IP]),
     "gl3_generate_sampled": (_I, [_P, _IP, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_float,
                                  ctypes.c_float, _FP, _IP]),

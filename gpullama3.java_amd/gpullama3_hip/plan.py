@@ -109,6 +109,11 @@ class HipMasterPlan:
         _ok(self.lib.gl3_generate_greedy(self.h, token, position, n_steps, L.iptr(out)))
         return out
 
+    def prefill(self, tokens, position):
+        """The prompt phase batched (gl3_prefill): K and V of tokens at position.., no logits."""
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        _ok(self.lib.gl3_prefill(self.h, L.iptr(t), t.size, position))
+
     def generate_from_prompt(self, prompt, position, n_gen):
         """The prompt forwarded on the device, then n_gen greedy tokens (gl3_generate_from_prompt)."""
         pr = np.ascontiguousarray(prompt, dtype=np.int32)

@@ -85,6 +85,8 @@ typedef enum gl3_tensor_kind {
                                       the persistent decode kernel */
 #define GL3_FLAG_TIMING 2u         /* record HIP events around every launch (gl3_get_timing) */
 #define GL3_FLAG_PHASE_TRACE 4u    /* every workgroup of the persistent kernel stamps every phase boundary */
+#define GL3_FLAG_STEPWISE_PROMPT 8u  /* generate calls forward the prompt one decode step per token (as the
+                                        reference does) instead of the batched prefill */
 
 /* Shape of the model.  Filled by the Java host from the reference's
  * Configuration (model/Configuration.java) — head_dim is
@@ -145,21 +147,35 @@ int gl3_forward(gl3_plan *p, int32_t token, int32_t position, float *logits_out,
  * with the sampler fixed to TENSOR_ARGMAX, so the logits never leave the GPU. */
 int gl3_generate_greedy(gl3_plan *p, int32_t token, int32_t position, int32_t n_steps, int32_t *tokens_out);
 
+/* The prompt phase of the reference's generation loop (InferenceEngine.java:88-131,
+ * :162-187: one forward per prompt token, logits unused), batched: the n tokens
+ * go through every layer in blocks of up to 512 rows (matrix products on the
+ * matrix cores, causal attention over the cache), leaving their K and V at
+ * positions position .. position + n - 1 and no logits.  A gl3_forward of the
+ * next token then continues as after n single forwards.  Requires head_dim 64,
+ * 96 or 128, every token in [0, vocab_size) and position + n <= context_length.
+ * Returns after the cache is written. */
+int gl3_prefill(gl3_plan *p, const int32_t *tokens, int32_t n, int32_t position);
+
 /* The reference's generation loop with the TENSOR_ARGMAX sampler, entirely on the
  * device (InferenceEngine.generateTokensGPULlama, inference/InferenceEngine.java:309-355):
  * forwards the n_prompt prompt tokens at positions position.. (their logits are
  * not used, as in the reference's prompt phase), then greedy steps; tokens_out
  * receives the n_gen generated tokens (the argmax after the last prompt token,
- * then after each generated one).  n_prompt + n_gen - 1 forwards in persistent
- * launches, no host round trip between them.  Requires every prompt token in
- * [0, vocab_size) and position + n_prompt + n_gen - 1 <= context_length. */
+ * then after each generated one).  All prompt tokens but the last go through the
+ * batched prefill of gl3_prefill (one decode step each with
+ * GL3_FLAG_STEPWISE_PROMPT, or when the shape has no prefill); the last prompt
+ * token and the generated ones are decode steps in persistent launches, no host
+ * round trip between them.  Requires every prompt token in [0, vocab_size) and
+ * position + n_prompt + n_gen - 1 <= context_length. */
 int gl3_generate_from_prompt(gl3_plan *p, const int32_t *prompt, int32_t n_prompt, int32_t position, int32_t n_gen,
                              int32_t *tokens_out);
 
 /* The reference's generation loop with a sampling Sampler, entirely on the
  * device (InferenceEngine.generateTokensGPULlama, inference/InferenceEngine.java:309-355,
  * with Sampler.selectSampler, inference/sampler/Sampler.java:74-122): the
- * n_prompt prompt tokens are forwarded from `position` (logits unused), then
+ * n_prompt prompt tokens are forwarded from `position` (logits unused; the
+ * prompt as in gl3_generate_from_prompt), then
  * each of the n_gen tokens is sampled on the device from the last step's
  * logits and forwarded: temperature 0 takes the first maximum (TENSOR_ARGMAX);
  * otherwise the logits are divided by the temperature and turned into

@@ -20,10 +20,10 @@ def small(key, n_layers=2, vocab=4096, ctx=512):
     return LAYER_SHAPES[key].with_(n_layers=n_layers, vocab_size=vocab, context_length=ctx)
 
 
-def build(shape, seed=7, flags=0, norm_init="random", kv_fp16=True, threads=0):
+def build(shape, seed=7, flags=0, norm_init="random", kv_fp16=True, threads=0, f16_exact=False):
     tensors = synth_model(shape, seed, norm_init=norm_init)
     plan = HipMasterPlan.initialize_plan(shape, tensors, flags=flags)
-    ref = orc.OracleModel(shape, tensors, kv_fp16=kv_fp16, n_threads=threads)
+    ref = orc.OracleModel(shape, tensors, kv_fp16=kv_fp16, f16_exact=f16_exact, n_threads=threads)
     return plan, ref, tensors
 
 
