@@ -111,7 +111,7 @@ struct gl3_plan {
   // batched prefill workspace, allocated on first use: residual rows, q/k/v
   // rows, and two pairs of hi / lo fp16 activation planes (a: normed rows and
   // attention output, b: SwiGLU output)
-  float *pf_x = nullptr, *pf_qkv = nullptr;
+  float *pf_x = nullptr, *pf_qkv = nullptr, *pf_part = nullptr;
   _Float16 *pf_ah = nullptr, *pf_al = nullptr, *pf_bh = nullptr, *pf_bl = nullptr;
   float *probs = nullptr;             // sampler scratch [vocab]
   float *coins = nullptr;             // sampler draws of the current generate call [context length]
@@ -882,7 +882,8 @@ static int run_prefill(gl3_plan *p, const int *d_tokens, int n, int pos0) {
     const size_t wa = (size_t)R * std::max(m.dim, m.q_dim), wb = (size_t)R * m.hidden;
     if ((rc = dev_alloc(p, &p->pf_x, (size_t)R * m.dim)) || (rc = dev_alloc(p, &p->pf_qkv, (size_t)R * (m.q_dim + 2 * m.kv_dim))) ||
         (rc = dev_alloc(p, &p->pf_ah, wa)) || (rc = dev_alloc(p, &p->pf_al, wa)) ||
-        (rc = dev_alloc(p, &p->pf_bh, wb)) || (rc = dev_alloc(p, &p->pf_bl, wb)))
+        (rc = dev_alloc(p, &p->pf_bh, wb)) || (rc = dev_alloc(p, &p->pf_bl, wb)) ||
+        (rc = dev_alloc(p, &p->pf_part, GL3_PREFILL_PART_FLOATS)))
       return rc;
   }
   hipStream_t s = p->stream;
@@ -893,13 +894,16 @@ static int run_prefill(gl3_plan *p, const int *d_tokens, int n, int pos0) {
     for (int l = 0; l < m.n_layers; ++l) {
       HIP_TRY(launch_rmsnorm_rows(p->pf_x, p->attn_norm[l], m.eps, m.dim, T, ah, al, s));
       HIP_TRY(launch_prefill_gemm(m.fmt, MODE_STORE, p->qkv[l].view(), m.q_dim + 2 * m.kv_dim, ah, al, T, p->pf_qkv,
-                                  nullptr, nullptr, s));
+                                  nullptr, nullptr, p->pf_part, s));
       HIP_TRY(launch_rope_kv_rows(m, l, p->pf_qkv, p0, T, s));
       HIP_TRY(launch_attn_rows(m, l, p->pf_qkv, p0, T, ah, al, s));
-      HIP_TRY(launch_prefill_gemm(m.fmt, MODE_RESIDUAL, p->wo[l].view(), m.dim, ah, al, T, p->pf_x, nullptr, nullptr, s));
+      HIP_TRY(launch_prefill_gemm(m.fmt, MODE_RESIDUAL, p->wo[l].view(), m.dim, ah, al, T, p->pf_x, nullptr, nullptr,
+                                  p->pf_part, s));
       HIP_TRY(launch_rmsnorm_rows(p->pf_x, p->ffn_norm[l], m.eps, m.dim, T, ah, al, s));
-      HIP_TRY(launch_prefill_gemm(m.fmt, MODE_SWIGLU, p->gu[l].view(), m.hidden, ah, al, T, nullptr, bh, bl, s));
-      HIP_TRY(launch_prefill_gemm(m.fmt, MODE_RESIDUAL, p->down[l].view(), m.dim, bh, bl, T, p->pf_x, nullptr, nullptr, s));
+      HIP_TRY(launch_prefill_gemm(m.fmt, MODE_SWIGLU, p->gu[l].view(), m.hidden, ah, al, T, nullptr, bh, bl, p->pf_part,
+                                  s));
+      HIP_TRY(launch_prefill_gemm(m.fmt, MODE_RESIDUAL, p->down[l].view(), m.dim, bh, bl, T, p->pf_x, nullptr, nullptr,
+                                  p->pf_part, s));
     }
   }
   return GL3_OK;

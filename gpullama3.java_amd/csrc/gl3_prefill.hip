@@ -16,6 +16,8 @@
 // weights enter as their int8 quants (exact in fp16), one MFMA pair per
 // 32-column block, and the block's scale multiplies the pair's fp32 result;
 // FP16 weights enter as they are.
+#include <algorithm>
+
 #include "gl3_internal.h"
 
 namespace gl3 {
@@ -33,86 +35,221 @@ __device__ __forceinline__ void put_split(_Float16 *hi, _Float16 *lo, size_t i, 
   lo[i] = (_Float16)(x - (float)h);
 }
 
-// 8 int8 quants (two dwords) as exact fp16 values
+typedef _Float16 ph2 __attribute__((ext_vector_type(2)));
+
+// 4 int8 quants (one dword) as 4 exact fp16 values: each byte, biased to
+// unsigned, becomes the low mantissa byte of fp16 0x64xx (= 1024 + u), and
+// 1152 = 1024 + 128 is subtracted (v_perm_b32 + packed fp16 subtraction).
+__device__ __forceinline__ void i8x4_to_h4(unsigned w, ph2 &lo, ph2 &hi) {
+  const unsigned u = w ^ 0x80808080u;
+  const unsigned a = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+  const unsigned b = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+  const ph2 bias = ph2{(_Float16)1152.0f, (_Float16)1152.0f};
+  lo = __builtin_bit_cast(ph2, a) - bias;
+  hi = __builtin_bit_cast(ph2, b) - bias;
+}
+
 __device__ __forceinline__ ph8 q8_to_h8(unsigned w0, unsigned w1) {
-  ph8 r;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    r[i] = (_Float16)(float)(signed char)((w0 >> (8 * i)) & 0xffu);
-    r[4 + i] = (_Float16)(float)(signed char)((w1 >> (8 * i)) & 0xffu);
-  }
-  return r;
+  ph2 a, b, c, d;
+  i8x4_to_h4(w0, a, b);
+  i8x4_to_h4(w1, c, d);
+  return ph8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+constexpr int GBT = 64;        // rows of X per workgroup tile
+constexpr int GBN = 128;       // rows of W per workgroup tile (SwiGLU: 64 gate + the 64 matching up rows)
+constexpr int GBK = 64;        // columns per stage (two Q8_0 blocks)
+constexpr int XSTR = GBK + 8;  // X tile row stride in LDS, halves (144 B: conflict-free 16-B reads by 16 rows)
+
+struct GemmArgs {
+  const uint8_t *wq;
+  const uint16_t *ws;
+  int N, K;                  // output columns (SwiGLU: hidden), reduction length
+  const _Float16 *xh, *xl;   // activations [T][K] as hi / lo planes
+  int T;
+  float *y;                  // MODE_STORE / MODE_RESIDUAL output [T][N]
+  _Float16 *yh, *yl;         // MODE_SWIGLU output planes [T][N]
+  float *part;               // split-K partials [ksplit][T][NW] (NW = N, SwiGLU 2N: gate then up)
+  int ksplit;
+};
+
+// Output element (t, n) of the matrix product, applied per mode.
+template <int MODE>
+__device__ __forceinline__ void gemm_store(const GemmArgs &g, int t, int n, float a, float up) {
+  const size_t i = (size_t)t * g.N + n;
+  if (MODE == MODE_STORE)
+    g.y[i] = a;
+  else if (MODE == MODE_RESIDUAL)
+    g.y[i] += a;
+  else
+    put_split(g.yh, g.yl, i, silu_ref(a) * up);  // InferenceCore.java:162-166
 }
 
 }  // namespace
 
-// Y[T][N] = X[T][K] . W[N][K]^T.  One wave computes a 16 (rows of X) x 64
-// (rows of W) tile as four 16 x 16 MFMA tiles; the four waves of a workgroup
-// take four consecutive 16-row groups of X over the same 64 rows of W (the
-// weights come through L1 once per workgroup).  MFMA operands: lane (hh, kb)
-// holds row hh of the A tile (a row of X) and column hh of the B tile (a row
-// of W), elements 8 kb .. 8 kb + 7 of the 32-column step; the result lane holds
-// rows 4 kb .. 4 kb + 3 of column hh.
-// MODE_STORE: Y = fp32; MODE_RESIDUAL: Y += fp32; MODE_SWIGLU: W holds gate
-// rows then up rows ([2N][K]) and the output is silu(gate) * up as hi / lo
-// fp16 planes Yh, Yl.
+// Y[T][N] = X[T][K] . W[N][K]^T on the matrix cores.  A workgroup computes a
+// 64 (rows of X) x 128 (rows of W) tile over its share of K, in stages of 64
+// columns: both operands go through LDS (global -> registers -> LDS, the next
+// stage's loads in flight during the current stage's products, two LDS
+// buffers, one barrier per stage).  Wave w owns W tile rows 32w .. 32w + 31
+// (SwiGLU: gate rows 16w .. 16w + 15 and the matching up rows, so that one lane
+// holds both values of an output) against all 64 rows of X: 2 x 4 MFMA tiles of
+// 16 x 16.  MFMA operands: lane (hh, kb) holds row hh of the A tile (a row of
+// X) and column hh of the B tile (a row of W), elements 8 kb .. 8 kb + 7 of the
+// 32-column block; the result lane holds rows 4 kb .. 4 kb + 3 of column hh.
+// With ksplit > 1, blockIdx.z takes K / ksplit columns and writes fp32
+// partials; gemm_reduce_kernel adds them in split order and applies the mode.
 template <int FMT, int MODE>
-__global__ __launch_bounds__(PBS) void gemm_kernel(const uint8_t *wq, const uint16_t *ws, int N, int K,
-                                                   const _Float16 *Xh, const _Float16 *Xl, int T, float *Y,
-                                                   _Float16 *Yh, _Float16 *Yl) {
-  constexpr int NP = MODE == MODE_SWIGLU ? 2 : 1;
-  const int wave = threadIdx.x / GL3_WAVE, lane = threadIdx.x % GL3_WAVE;
+__global__ __launch_bounds__(PBS) void gemm_kernel(GemmArgs g) {
+  constexpr bool SW = MODE == MODE_SWIGLU;
+  constexpr int WSB = FMT == FMT_Q8 ? 80 : 144;    // W tile row stride in LDS, bytes (conflict-free reads)
+  constexpr int WLD = FMT == FMT_Q8 ? 2 : 4;       // 16-byte W loads per thread per stage
+  __shared__ __align__(16) _Float16 xs[2][2][GBT * XSTR];  // [buffer][hi / lo][row * XSTR + column]
+  __shared__ __align__(16) uint8_t wsm[2][GBN * WSB];      // [buffer][row * WSB + byte]
+  __shared__ unsigned ssm[2][GBN];                         // Q8_0: the row's two block scales of the stage
+
+  const int tid = threadIdx.x, wave = tid / GL3_WAVE, lane = tid % GL3_WAVE;
   const int hh = lane % 16, kb = lane / 16;
-  const int n0 = blockIdx.x * 64, t0 = blockIdx.y * 64 + wave * 16;
-  if (t0 >= T) return;  // no row of this wave is in the block (nothing below synchronizes)
-  const size_t trow = (size_t)min(t0 + hh, T - 1);  // rows past T repeat the last; their results are dropped
-  const _Float16 *xh = Xh + trow * K + 8 * kb, *xl = Xl + trow * K + 8 * kb;
-  size_t wrow[NP][4];
+  const int n0 = blockIdx.x * (SW ? GBN / 2 : GBN);
+  const int t0 = blockIdx.y * GBT;
+  const int kper = g.K / g.ksplit, kbeg = blockIdx.z * kper, nst = kper / GBK;
+
+  // global W row of LDS tile row r (rows past the matrix repeat its last row; their results are dropped)
+  auto wrow = [&](int r) -> size_t {
+    if (SW) return r < GBN / 2 ? (size_t)min(n0 + r, g.N - 1) : (size_t)g.N + min(n0 + r - GBN / 2, g.N - 1);
+    return (size_t)min(n0 + r, g.N - 1);
+  };
+  // loaders: X rows tid / 8 and tid / 8 + 32, 16-byte chunk tid % 8, both planes;
+  // W (Q8_0: 64 bytes per row, 4 threads a row; F16: 128 bytes, 8 threads a row)
+  const int xr = tid / 8, xc = 8 * (tid % 8);
+  const size_t xo0 = (size_t)min(t0 + xr, g.T - 1) * g.K + xc, xo1 = (size_t)min(t0 + xr + 32, g.T - 1) * g.K + xc;
+  constexpr int TPR = FMT == FMT_Q8 ? 4 : 8;  // threads per W row
+  constexpr int RPL = PBS / TPR;              // W rows per load round
+  size_t wo[WLD];
 #pragma unroll
-  for (int p = 0; p < NP; ++p)
+  for (int i = 0; i < WLD; ++i)
+    wo[i] = wrow(tid / TPR + RPL * i) * (size_t)g.K * (FMT == FMT_Q8 ? 1 : 2) + 16 * (tid % TPR);
+  const size_t so = FMT == FMT_Q8 && tid < GBN ? wrow(tid) * (size_t)(g.K / 32) : 0;
+
+  u32x4 rx[4], rw[WLD];
+  unsigned rs = 0;
+  auto gload = [&](int k0) {
+    rx[0] = *(const u32x4 *)(g.xh + xo0 + k0);
+    rx[1] = *(const u32x4 *)(g.xl + xo0 + k0);
+    rx[2] = *(const u32x4 *)(g.xh + xo1 + k0);
+    rx[3] = *(const u32x4 *)(g.xl + xo1 + k0);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) wrow[p][j] = (size_t)min(n0 + 16 * j + hh, N - 1) + (size_t)p * N;
-  pf4 acc[NP][4];
+    for (int i = 0; i < WLD; ++i) rw[i] = *(const u32x4 *)(g.wq + wo[i] + (size_t)k0 * (FMT == FMT_Q8 ? 1 : 2));
+    if (FMT == FMT_Q8 && tid < GBN) rs = *(const unsigned *)(g.ws + so + k0 / 32);
+  };
+  auto lstore = [&](int buf) {
+    *(u32x4 *)&xs[buf][0][xr * XSTR + xc] = rx[0];
+    *(u32x4 *)&xs[buf][1][xr * XSTR + xc] = rx[1];
+    *(u32x4 *)&xs[buf][0][(xr + 32) * XSTR + xc] = rx[2];
+    *(u32x4 *)&xs[buf][1][(xr + 32) * XSTR + xc] = rx[3];
 #pragma unroll
-  for (int p = 0; p < NP; ++p)
+    for (int i = 0; i < WLD; ++i) *(u32x4 *)&wsm[buf][(tid / TPR + RPL * i) * WSB + 16 * (tid % TPR)] = rw[i];
+    if (FMT == FMT_Q8 && tid < GBN) ssm[buf][tid] = rs;
+  };
+
+  // this wave's two 16-row groups of the W tile
+  const int rj[2] = {SW ? 16 * wave : 32 * wave, SW ? GBN / 2 + 16 * wave : 32 * wave + 16};
+  pf4 acc[2][4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[p][j] = pf4{0.0f, 0.0f, 0.0f, 0.0f};
-  for (int k0 = 0; k0 < K; k0 += 32) {
-    const ph8 ahi = *(const ph8 *)(xh + k0), alo = *(const ph8 *)(xl + k0);
+  for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int p = 0; p < NP; ++p)
+    for (int i = 0; i < 4; ++i) acc[j][i] = pf4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  gload(kbeg);
+  lstore(0);
+  __syncthreads();
+  for (int st = 0; st < nst; ++st) {
+    const int buf = st & 1;
+    if (st + 1 < nst) gload(kbeg + (st + 1) * GBK);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const size_t n = wrow[p][j];
+    for (int b = 0; b < 2; ++b) {  // the stage's two 32-column blocks
+      ph8 ah[4], al[4], bw[2];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        ah[i] = *(const ph8 *)&xs[buf][0][(16 * i + hh) * XSTR + 32 * b + 8 * kb];
+        al[i] = *(const ph8 *)&xs[buf][1][(16 * i + hh) * XSTR + 32 * b + 8 * kb];
+      }
+      float sc[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int r = rj[j] + hh;
         if (FMT == FMT_Q8) {
-          const uint2 w = *(const uint2 *)(wq + n * K + k0 + 8 * kb);
-          const ph8 b = q8_to_h8(w.x, w.y);
-          pf4 tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b, pf4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-          tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b, tmp, 0, 0, 0);
-          const float sc = h2f(ws[n * (K / 32) + k0 / 32]);
-#pragma unroll
-          for (int v = 0; v < 4; ++v) acc[p][j][v] = fmaf(tmp[v], sc, acc[p][j][v]);
+          const uint2 w = *(const uint2 *)&wsm[buf][r * WSB + 32 * b + 8 * kb];
+          bw[j] = q8_to_h8(w.x, w.y);
+          sc[j] = h2f((uint16_t)(ssm[buf][r] >> (16 * b)));
         } else {
-          const ph8 b = *(const ph8 *)(wq + (n * K + k0 + 8 * kb) * 2);
-          acc[p][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b, acc[p][j], 0, 0, 0);
-          acc[p][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b, acc[p][j], 0, 0, 0);
+          bw[j] = *(const ph8 *)&wsm[buf][r * WSB + 2 * (32 * b + 8 * kb)];
         }
       }
-  }
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (FMT == FMT_Q8) {
+            pf4 tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bw[j], pf4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+            tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bw[j], tmp, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[j][i][v] = fmaf(tmp[v], sc[j], acc[j][i][v]);
+          } else {
+            acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bw[j], acc[j][i], 0, 0, 0);
+            acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bw[j], acc[j][i], 0, 0, 0);
+          }
+        }
+    }
+    if (st + 1 < nst) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  const int NW = SW ? 2 * g.N : g.N;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      const int t = t0 + 4 * kb + v, n = n0 + 16 * j + hh;
-      if (t >= T || n >= N) continue;
-      const size_t i = (size_t)t * N + n;
-      if (MODE == MODE_STORE)
-        Y[i] = acc[0][j][v];
-      else if (MODE == MODE_RESIDUAL)
-        Y[i] += acc[0][j][v];
-      else
-        put_split(Yh, Yl, i, silu_ref(acc[0][j][v]) * acc[NP - 1][j][v]);  // InferenceCore.java:162-166
+      const int t = t0 + 16 * i + 4 * kb + v;
+      if (t >= g.T) continue;
+      if (SW) {
+        const int n = n0 + 16 * wave + hh;
+        if (n >= g.N) continue;
+        if (g.ksplit == 1) {
+          gemm_store<MODE>(g, t, n, acc[0][i][v], acc[1][i][v]);
+        } else {
+          float *pp = g.part + ((size_t)blockIdx.z * g.T + t) * NW;
+          pp[n] = acc[0][i][v];
+          pp[g.N + n] = acc[1][i][v];
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int n = n0 + 32 * wave + 16 * j + hh;
+          if (n >= g.N) continue;
+          if (g.ksplit == 1)
+            gemm_store<MODE>(g, t, n, acc[j][i][v], 0.0f);
+          else
+            g.part[((size_t)blockIdx.z * g.T + t) * NW + n] = acc[j][i][v];
+        }
+      }
     }
+}
+
+// Sum of the split-K partials in split order, then the mode's output.
+template <int MODE>
+__global__ __launch_bounds__(PBS) void gemm_reduce_kernel(GemmArgs g) {
+  const size_t i = (size_t)blockIdx.x * PBS + threadIdx.x;
+  if (i >= (size_t)g.T * g.N) return;
+  const int t = (int)(i / g.N), n = (int)(i % g.N);
+  const int NW = MODE == MODE_SWIGLU ? 2 * g.N : g.N;
+  float a = 0.0f, u = 0.0f;
+  for (int s = 0; s < g.ksplit; ++s) {
+    const float *pp = g.part + ((size_t)s * g.T + t) * NW;
+    a += pp[n];
+    if (MODE == MODE_SWIGLU) u += pp[g.N + n];
+  }
+  gemm_store<MODE>(g, t, n, a, u);
 }
 
 // Residual-stream rows of the block: the embedding rows of its tokens (InferenceCore.java:68)
@@ -285,18 +422,34 @@ __global__ __launch_bounds__(PBS) void attn_rows_kernel(ModelDev m, int layer, c
 }
 
 bool prefill_supported(const ModelDev &m) {
-  return (m.hd == 64 || m.hd == 96 || m.hd == 128) && m.dim % 32 == 0 && m.q_dim % 32 == 0 && m.hidden % 32 == 0 &&
-         m.rope_cos != nullptr;
+  return (m.hd == 64 || m.hd == 96 || m.hd == 128) && m.dim % GBK == 0 && m.q_dim % GBK == 0 &&
+         m.hidden % GBK == 0 && m.rope_cos != nullptr;
+}
+
+// K splits of a product with `base` output tiles: none when the tiles alone
+// give every CU a workgroup, else enough for ~512 workgroups, each split at
+// least 4 stages long and a divisor of the K / 64 stages.  The partials then
+// take at most (512 + base) * 64 * 128 floats (GL3_PREFILL_PART_FLOATS).
+static int gemm_ksplit(int base, int K) {
+  if (base >= 256) return 1;
+  int s = std::min((512 + base - 1) / base, K / (4 * GBK));
+  while (s > 1 && (K / GBK) % s) --s;
+  return std::max(s, 1);
 }
 
 hipError_t launch_prefill_gemm(int fmt, int mode, const Mat &W, int N, const _Float16 *Xh, const _Float16 *Xl, int T,
-                               float *Y, _Float16 *Yh, _Float16 *Yl, hipStream_t s) {
-  if (W.cols % 32 != 0 || T <= 0 || N <= 0) return hipErrorInvalidValue;
-  const dim3 grid((N + 63) / 64, (T + 63) / 64);
-#define GL3_GEMM(F, M)                                                                                          \
-  if (fmt == F && mode == M) {                                                                                  \
-    hipLaunchKernelGGL((gemm_kernel<F, M>), grid, dim3(PBS), 0, s, W.q, W.s, N, W.cols, Xh, Xl, T, Y, Yh, Yl);  \
-    return hipGetLastError();                                                                                   \
+                               float *Y, _Float16 *Yh, _Float16 *Yl, float *part, hipStream_t s) {
+  if (W.cols % GBK != 0 || T <= 0 || N <= 0) return hipErrorInvalidValue;
+  GemmArgs g{W.q, W.s, N, W.cols, Xh, Xl, T, Y, Yh, Yl, part, 1};
+  const int nt = mode == MODE_SWIGLU ? (N + GBN / 2 - 1) / (GBN / 2) : (N + GBN - 1) / GBN, tt = (T + GBT - 1) / GBT;
+  g.ksplit = gemm_ksplit(nt * tt, g.K);
+  const dim3 grid(nt, tt, g.ksplit);
+  const unsigned rgrid = (unsigned)(((size_t)T * N + PBS - 1) / PBS);
+#define GL3_GEMM(F, M)                                                                   \
+  if (fmt == F && mode == M) {                                                           \
+    hipLaunchKernelGGL((gemm_kernel<F, M>), grid, dim3(PBS), 0, s, g);                   \
+    if (g.ksplit > 1) hipLaunchKernelGGL((gemm_reduce_kernel<M>), dim3(rgrid), dim3(PBS), 0, s, g); \
+    return hipGetLastError();                                                            \
   }
   GL3_GEMM(FMT_Q8, MODE_STORE) GL3_GEMM(FMT_Q8, MODE_RESIDUAL) GL3_GEMM(FMT_Q8, MODE_SWIGLU)
   GL3_GEMM(FMT_F16, MODE_STORE) GL3_GEMM(FMT_F16, MODE_RESIDUAL) GL3_GEMM(FMT_F16, MODE_SWIGLU)
