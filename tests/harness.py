@@ -54,3 +54,26 @@ def prefill_from_device(plan, ref, shape, npos, seed=3):
         rk, rv = ref.kv(l)
         rk[:npos] = k.view(np.float16)
         rv[:npos] = v.view(np.float16)
+
+
+TOL_KV = 4e-3  # K/V of a prefill: max |d| over the layer's largest magnitude
+
+
+def check_kv(plan, ref, shape, pos0, npos):
+    """Device K/V at [pos0, pos0 + npos) of every layer against the oracle's."""
+    worst = 0.0
+    for l in range(shape.n_layers):
+        k, v = plan.read_kv(l, pos0, npos)
+        rk, rv = ref.kv(l)
+        for dev, want, what in ((k, rk, "K"), (v, rv, "V")):
+            got = dev.view(np.float16).astype(np.float32)
+            exp = want[pos0:pos0 + npos]
+            scale = float(np.max(np.abs(exp)))
+            d = np.abs(got - exp)
+            rel = float(d.max()) / scale
+            worst = max(worst, rel)
+            if rel > TOL_KV:
+                p, c = np.unravel_index(int(np.argmax(d)), d.shape)
+                raise AssertionError(f"layer {l} {what} position {pos0 + p} column {c}: {got[p, c]} vs "
+                                     f"{exp[p, c]} (max |d| / max |ref| = {rel:.2e})")
+    return worst

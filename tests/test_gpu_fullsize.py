@@ -11,7 +11,10 @@ differently cannot make the sequences drift apart.
 * Llama-3.2-1B Q8_0 (untied Q8_0 classifier, FP16 embeddings): the same
   workload, and 8 greedy steps from each start position of the benchmark's
   segments across 0-2047 over an fp16 N(0,1) history.
-* Qwen3-0.6B Q8_0: 512-token prompt, 256 greedy steps (positions 0-767).
+* Qwen3-0.6B Q8_0: 512-token prompt, 256 greedy steps (positions 0-767); the
+  prompt as the generate calls run it, 511 tokens through the batched prefill
+  (K and V checked against the oracle's at every position and layer, within
+  4e-3 of the layer's largest magnitude), the last one decoded.
 * Phi-3-mini FP16: 34 steps at positions 4062-4095 over an fp16 N(0,1) history.
 * Llama-3.1-8B Q8_0: 4 steps from each KV fill 8192, 16384 and 32768 over an
   fp16 N(0,1) history (32 full-size layers; 16 and 32 attention splits of 1024
@@ -27,7 +30,7 @@ import bench
 import oracle.oracle as orc
 from gpullama3_hip import HipMasterPlan
 from gpullama3_hip.model import CONFIGS, synth_model
-from harness import prefill_from_device, top2_margin
+from harness import check_kv, prefill_from_device, top2_margin
 
 pytestmark = pytest.mark.gpu
 
@@ -35,11 +38,20 @@ TOL = 2e-2
 THREADS = min(16, os.cpu_count() or 1)
 
 
-def steps(plan, ref, prompt, n_gen, start):
-    """Teacher-forced steps from `start`; returns (worst |d|/std, greedy checks, near ties)."""
+def steps(plan, ref, prompt, n_gen, start, prefill=False):
+    """Teacher-forced steps from `start`; returns (worst |d|/std, greedy checks, near ties).
+    prefill: all prompt tokens but the last go through the batched prefill."""
     worst, checked, ties = 0.0, 0, 0
     tok = int(prompt[0])
-    for i in range(len(prompt) + n_gen):
+    first = 0
+    if prefill and len(prompt) > 1:
+        plan.prefill(prompt[:-1], start)
+        for i, t in enumerate(prompt[:-1]):
+            ref.forward(int(t), start + i)
+        kvd = check_kv(plan, ref, plan.shape, start, len(prompt) - 1)
+        print(f"  prefill of {len(prompt) - 1} tokens: K/V max|d|/max|ref| {kvd:.2e}", flush=True)
+        first, tok = len(prompt) - 1, int(prompt[-1])
+    for i in range(first, len(prompt) + n_gen):
         pos = start + i
         lg, am = plan.forward(tok, pos)
         rl = ref.forward(tok, pos)
@@ -58,14 +70,14 @@ def steps(plan, ref, prompt, n_gen, start):
     return worst, checked, ties
 
 
-def run(shape, prompt, n_gen, start=0, seed=1234):
-    print(f"[case] {shape.name} prompt {len(prompt)} gen {n_gen} start {start}", flush=True)
+def run(shape, prompt, n_gen, start=0, seed=1234, prefill=False):
+    print(f"[case] {shape.name} prompt {len(prompt)} gen {n_gen} start {start} prefill {prefill}", flush=True)
     tensors = synth_model(shape, seed, norm_init="ones")
     plan = HipMasterPlan.initialize_plan(shape, tensors)
     ref = orc.OracleModel(shape, tensors, kv_fp16=False, n_threads=THREADS)
     if start:
         prefill_from_device(plan, ref, shape, start, seed=start)
-    worst, checked, ties = steps(plan, ref, prompt, n_gen, start)
+    worst, checked, ties = steps(plan, ref, prompt, n_gen, start, prefill=prefill)
     print(f"  max|d|/std {worst:.2e}; greedy ids equal at {checked} steps, {ties} within the tolerance", flush=True)
     plan.free_execution_plan()
     ref.close()
@@ -107,7 +119,7 @@ def test_llama1b_q8_benchmark_segments(gpu):
 def test_qwen3_prompt_then_greedy(gpu):
     shape = CONFIGS["qwen3_06b_q8"].with_(context_length=768)
     prompt = np.random.default_rng(8).integers(0, shape.vocab_size, 512)
-    assert run(shape, prompt, 256) > 0
+    assert run(shape, prompt, 256, prefill=True) > 0
 
 
 def test_phi3_long_context(gpu):

@@ -22,35 +22,14 @@ import pytest
 
 import oracle.oracle as orc
 from gpullama3_hip import _lib as L
-from harness import build, small, top2_margin
+from harness import build, check_kv, small, top2_margin
 
 pytestmark = pytest.mark.gpu
 
 TOL_TIGHT = 2e-3
 TOL_REF = 2e-2
-TOL_KV = 4e-3
 
 SCHEDULES = {"persistent": 0, "graph": L.FLAG_PHASE_KERNELS}
-
-
-def check_kv(plan, ref, shape, pos0, npos):
-    """Device K/V at [pos0, pos0 + npos) of every layer against the oracle's."""
-    worst = 0.0
-    for l in range(shape.n_layers):
-        k, v = plan.read_kv(l, pos0, npos)
-        rk, rv = ref.kv(l)
-        for dev, want, what in ((k, rk, "K"), (v, rv, "V")):
-            got = dev.view(np.float16).astype(np.float32)
-            exp = want[pos0:pos0 + npos]
-            scale = float(np.max(np.abs(exp)))
-            d = np.abs(got - exp)
-            rel = float(d.max()) / scale
-            worst = max(worst, rel)
-            if rel > TOL_KV:
-                p, c = np.unravel_index(int(np.argmax(d)), d.shape)
-                raise AssertionError(f"layer {l} {what} position {pos0 + p} column {c}: {got[p, c]} vs "
-                                     f"{exp[p, c]} (max |d| / max |ref| = {rel:.2e})")
-    return worst
 
 
 def teacher_forced(plan, ref, tok, pos, n, tol=TOL_TIGHT):
