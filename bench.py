@@ -328,7 +328,7 @@ def prefill_flops(shape, n, pos0=0):
     return s.n_layers * (per_tok * n + 4 * s.head_dim * s.n_heads * positions)
 
 
-def prompt_workload(seed, key="qwen3_06b_q8", n_prompt=512, n_gen=256):
+def prompt_workload(seed, key="qwen3_06b_q8", n_prompt=512, n_gen=256, stepwise=True):
     """Qwen3-0.6B Q8_0 with a 512-token random prompt and 256 greedy tokens
     from position 0, tokens/s = (prompt + generated) / wall time as the
     reference counts it: the prompt through the batched prefill, and the same
@@ -343,7 +343,8 @@ def prompt_workload(seed, key="qwen3_06b_q8", n_prompt=512, n_gen=256):
     out = {"workload": f"{key}: {shape.name}, {n_prompt}-token random prompt then {n_gen} greedy tokens from "
                        f"position 0", "prompt_tokens": n_prompt, "generated_tokens": n_gen}
     toks = {}
-    for name, flags in (("prefill", 0), ("stepwise", L.FLAG_STEPWISE_PROMPT)):
+    runs = (("prefill", 0), ("stepwise", L.FLAG_STEPWISE_PROMPT)) if stepwise else (("prefill", 0),)
+    for name, flags in runs:
         plan = HipMasterPlan.initialize_plan(shape, tensors, flags=flags)
         plan.generate_from_prompt(prompt, 0, 4)  # warm the path
         plan.reset()
@@ -365,7 +366,8 @@ def prompt_workload(seed, key="qwen3_06b_q8", n_prompt=512, n_gen=256):
                                       "twice the MFMA work (hi and lo fp16 parts of the activations)"})
         out[name] = r
         plan.free_execution_plan()
-    out["tokens_equal"] = bool(np.array_equal(toks["prefill"], toks["stepwise"]))
+    if stepwise:
+        out["tokens_equal"] = bool(np.array_equal(toks["prefill"], toks["stepwise"]))
     return out
 
 
@@ -383,6 +385,9 @@ def main():
     ap.add_argument("--steps-8b", type=int, default=128, help="greedy steps at each 8B KV fill")
     ap.add_argument("--no-8b", action="store_true", help="leave out the Llama-3.1-8B part of the line")
     ap.add_argument("--no-prompt", action="store_true", help="leave out the Qwen3 prompt workload")
+    ap.add_argument("--prompt-only", default=None, metavar="CONFIG",
+                    help="run only the prompt workload (512-token prompt through the batched prefill, then 256 "
+                         "greedy tokens) on CONFIG and print its JSON object")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only the plain copy kernel used to calibrate rocprofv3 byte counters")
@@ -402,6 +407,10 @@ def main():
 
     from gpullama3_hip import device_name
     from gpullama3_hip import _lib as L
+
+    if args.prompt_only:
+        print(json.dumps(prompt_workload(args.seed, key=args.prompt_only, stepwise=False)), flush=True)
+        return
 
     starts = [int(v) for v in args.starts.split(",")] if args.starts else None
     log(f"device: {device_name()}")
