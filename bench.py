@@ -242,6 +242,26 @@ def attention_rate(plan, shape, pos, reps=20):
             "achieved_gbs": round(kv / (ms * 1e-3) / 1e9, 1), "frac": round(kv / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def attention_only(seed, key="llama8b_q8", reps=50):
+    """The standalone flash-decode attention kernel of the Llama-3.1-8B shape at
+    each KV fill (fp16 N(0,1) history), without any decode step: a process that
+    a kernel-trace profiler can follow from start to exit."""
+    from gpullama3_hip import HipMasterPlan
+    from gpullama3_hip import _lib as L
+    from gpullama3_hip.model import CONFIGS, synth_model
+
+    shape = CONFIGS[key].with_(n_layers=1, context_length=max(FILLS_8B) + 16)
+    plan = HipMasterPlan.initialize_plan(shape, synth_model(shape, seed, norm_init="ones"),
+                                         flags=L.FLAG_PHASE_KERNELS)
+    out = []
+    for pos in FILLS_8B:
+        plan.fill_kv_normal(seed + pos, pos)
+        out.append(attention_rate(plan, shape, pos, reps))
+    plan.free_execution_plan()
+    return {"workload": f"{key}: standalone attention kernel, one layer, {reps} launches at each KV fill",
+            "attention_kernel": out}
+
+
 def bench_config(key, steps, warmup, seed, schedule, starts=None, with_attention=False):
     from gpullama3_hip import HipMasterPlan
     from gpullama3_hip import _lib as L
@@ -385,6 +405,9 @@ def main():
     ap.add_argument("--steps-8b", type=int, default=128, help="greedy steps at each 8B KV fill")
     ap.add_argument("--no-8b", action="store_true", help="leave out the Llama-3.1-8B part of the line")
     ap.add_argument("--no-prompt", action="store_true", help="leave out the Qwen3 prompt workload")
+    ap.add_argument("--attention-only", action="store_true",
+                    help="run only the standalone attention kernel of the Llama-3.1-8B shape at each KV fill and "
+                         "print its JSON object")
     ap.add_argument("--prompt-only", default=None, metavar="CONFIG",
                     help="run only the prompt workload (512-token prompt through the batched prefill, then 256 "
                          "greedy tokens) on CONFIG and print its JSON object")
@@ -408,6 +431,9 @@ def main():
     from gpullama3_hip import device_name
     from gpullama3_hip import _lib as L
 
+    if args.attention_only:
+        print(json.dumps(attention_only(args.seed)), flush=True)
+        return
     if args.prompt_only:
         print(json.dumps(prompt_workload(args.seed, key=args.prompt_only, stepwise=False)), flush=True)
         return
