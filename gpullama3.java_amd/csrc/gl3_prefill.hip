@@ -339,85 +339,136 @@ __global__ __launch_bounds__(PBS) void rope_kv_rows_kernel(ModelDev m, int layer
   }
 }
 
-// Causal attention of the block's rows, one wave per (row, query head), over
-// positions 0 .. p0 + t of the cache (InferenceCore.java:105-144: scores
-// q.k / sqrt(head_dim), softmax, weighted sum of v), as an online softmax over
-// chunks of 64 positions: lane j scores position c0 + j; then lane d
-// accumulates output dims d and d + 64 over the chunk, 16 positions of its V
-// dims per 32-byte read of the transposed V blocks.  Output as hi / lo planes.
+// Causal attention of the block's rows on the matrix cores (InferenceCore.java:105-144:
+// scores q.k / sqrt(head_dim), softmax over positions 0 .. pos, weighted sum of
+// v), flash style: one wave per (16 query rows, query head), over 16-position
+// tiles of the cache up to the block's last row.  Per tile:
+//   S^T[16 pos][16 rows] = K[16][hd] . Q^T    v_mfma_f32_16x16x32_f16 (q as hi + lo fp16)
+//   online softmax per row (a column of S^T: the four lanes l, l^16, l^32, l^48)
+//   O[16 rows][hd]     += P[16][16] . V        v_mfma_f32_16x16x16_f16 (p as hi + lo fp16)
+// S^T puts the positions on the rows so that P comes out of the first product
+// already in the A-operand layout of the second.  The next tile's K and V are
+// loaded while the current one is computed.  Positions past a row's own are
+// masked (and V past the block's last row zeroed: cache rows there may hold
+// anything).  Output as hi / lo planes.
 template <int HD>
 __global__ __launch_bounds__(PBS) void attn_rows_kernel(ModelDev m, int layer, const float *QKV, int p0, int T,
                                                         _Float16 *Oh, _Float16 *Ol) {
-  __shared__ float qs[PBS / GL3_WAVE][HD];
-  constexpr int DPL = (HD + GL3_WAVE - 1) / GL3_WAVE;  // output dims per lane
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  constexpr int NC = HD / 32, NB = HD / 16;
   const int wave = threadIdx.x / GL3_WAVE, lane = threadIdx.x % GL3_WAVE;
-  const int item = blockIdx.x * (PBS / GL3_WAVE) + wave;
-  const int t = min(item / m.n_heads, T - 1), h = item % m.n_heads;
-  const bool valid = item < T * m.n_heads;
-  const float *q = QKV + (size_t)t * (m.q_dim + 2 * m.kv_dim) + h * HD;
-  for (int d = lane; d < HD; d += GL3_WAVE) qs[wave][d] = q[d];
-  __syncthreads();  // every wave reaches it: invalid items are cut below
-  if (!valid) return;
-  const int kvh = h / (m.n_heads / m.n_kv), pos = p0 + t;
-  const uint16_t *kc = m.kc + ((size_t)layer * m.n_kv + kvh) * m.ctxp * HD;
-  const uint16_t *vt = m.vc + ((size_t)layer * m.n_kv + kvh) * HD * m.ctxp;
-  float o[DPL];
+  const int hh = lane % 16, kb = lane / 16;
+  const int G = m.n_heads / m.n_kv;
+  const int item = blockIdx.x * (PBS / GL3_WAVE) + wave;  // ((row block * n_kv) + kv head) * G + group member
+  const int g = item % G, kvh = (item / G) % m.n_kv, rb = item / (G * m.n_kv);
+  if (rb * 16 >= T) return;  // the whole wave leaves; nothing below synchronizes the workgroup
+  const int h = kvh * G + g, t0 = rb * 16;
+  const int last = p0 + min(t0 + 15, T - 1);        // last position any row of the block attends
+  const int qpos = min(p0 + t0 + hh, last);          // position of this lane's query row (column hh)
+  const int stride = m.q_dim + 2 * m.kv_dim;
+  // q of row t0 + hh as the B operand (column hh), dims 32c + 8kb .. + 7, hi and lo parts
+  ph8 qh[NC], ql[NC];
+  {
+    const float *qr = QKV + (size_t)min(t0 + hh, T - 1) * stride + h * HD;
 #pragma unroll
-  for (int i = 0; i < DPL; ++i) o[i] = 0.0f;
-  float mrun = -INFINITY, lrun = 0.0f;
-  for (int c0 = 0; c0 <= pos; c0 += GL3_WAVE) {
-    const int p = c0 + lane;
-    float s = -INFINITY;
-    if (p <= pos) {
-      const uint16_t *kr = kc + (size_t)p * HD;
-      float a = 0.0f;
+    for (int c = 0; c < NC; ++c) {
+      const float4 a = *(const float4 *)(qr + 32 * c + 8 * kb), b = *(const float4 *)(qr + 32 * c + 8 * kb + 4);
+      const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-      for (int d = 0; d < HD; d += 8) {
-        const u32x4 w = *(const u32x4 *)(kr + d);
-        a = fmaf(qs[wave][d + 0], h2f_lo(w.x), a);
-        a = fmaf(qs[wave][d + 1], h2f_hi(w.x), a);
-        a = fmaf(qs[wave][d + 2], h2f_lo(w.y), a);
-        a = fmaf(qs[wave][d + 3], h2f_hi(w.y), a);
-        a = fmaf(qs[wave][d + 4], h2f_lo(w.z), a);
-        a = fmaf(qs[wave][d + 5], h2f_hi(w.z), a);
-        a = fmaf(qs[wave][d + 6], h2f_lo(w.w), a);
-        a = fmaf(qs[wave][d + 7], h2f_hi(w.w), a);
-      }
-      s = a / m.sqrt_hd;
-    }
-    const float mn = fmaxf(mrun, wave_max(s));
-    const float cf = mrun == -INFINITY ? 0.0f : __expf(mrun - mn);
-    const float e = s == -INFINITY ? 0.0f : __expf(s - mn);
-    lrun = lrun * cf + wave_sum(e);
-    mrun = mn;
-#pragma unroll
-    for (int i = 0; i < DPL; ++i) o[i] *= cf;
-    const int ng = (min(GL3_WAVE, pos + 1 - c0) + 15) / 16;  // 16-position groups of the chunk
-    for (int g = 0; g < ng; ++g) {
-      const int pb = c0 + 16 * g;  // first position of the group (a multiple of 16)
-#pragma unroll
-      for (int i = 0; i < DPL; ++i) {
-        const int d = lane + GL3_WAVE * i;
-        if (d >= HD) continue;
-        const u32x4 *src = (const u32x4 *)(vt + ((size_t)(pb / 16) * HD + d) * 16);
-        const u32x4 w0 = src[0], w1 = src[1];
-        const unsigned wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-        float acc = o[i];
-#pragma unroll
-        for (int k = 0; k < 16; ++k) {
-          // positions past pos (e = 0) are skipped: their cache entries may be anything, inf or nan included
-          const float pk = readlane_f(e, 16 * g + k);
-          if (pb + k <= pos) acc = fmaf(pk, k % 2 ? h2f_hi(wv[k / 2]) : h2f_lo(wv[k / 2]), acc);
-        }
-        o[i] = acc;
+      for (int i = 0; i < 8; ++i) {
+        const _Float16 hv = (_Float16)x[i];
+        qh[c][i] = hv;
+        ql[c][i] = (_Float16)(x[i] - (float)hv);
       }
     }
   }
-  const size_t ob = (size_t)t * m.q_dim + (size_t)h * HD;
+  const uint16_t *kc = m.kc + ((size_t)layer * m.n_kv + kvh) * m.ctxp * HD;
+  const uint2 *vt = (const uint2 *)(m.vc + ((size_t)layer * m.n_kv + kvh) * HD * m.ctxp);
+  pf4 O[NB];
 #pragma unroll
-  for (int i = 0; i < DPL; ++i) {
-    const int d = lane + GL3_WAVE * i;
-    if (d < HD) put_split(Oh, Ol, ob + d, o[i] / lrun);
+  for (int b = 0; b < NB; ++b) O[b] = pf4{0.0f, 0.0f, 0.0f, 0.0f};
+  float mrun = -INFINITY, lrun = 0.0f;
+  // tile operands: K rows ts + hh (A: row hh, dims 32c + 8kb ..), V dims 16b + hh at positions 4kb .. 4kb + 3 (B)
+  ph8 kw[NC];
+  uint2 vw[NB];
+  auto load = [&](int ts, ph8 (&k)[NC], uint2 (&v)[NB]) {
+    const uint16_t *kr = kc + (size_t)(ts + hh) * HD;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) k[c] = *(const ph8 *)(kr + 32 * c + 8 * kb);
+    const uint2 *vb = vt + (size_t)(ts / 16) * HD * 4;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) v[b] = vb[(16 * b + hh) * 4 + kb];
+  };
+  load(0, kw, vw);
+  for (int ts = 0; ts <= last; ts += 16) {
+    ph8 kn[NC];
+    uint2 vn[NB];
+    if (ts + 16 <= last) load(ts + 16, kn, vn);  // the next tile in flight during this one
+    pf4 sacc = pf4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kw[c], qh[c], sacc, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kw[c], ql[c], sacc, 0, 0, 0);
+    }
+    // lane: positions ts + 4kb + v, query row hh
+    float sv[4], mx = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      sv[v] = ts + 4 * kb + v <= qpos ? sacc[v] / m.sqrt_hd : -INFINITY;
+      mx = fmaxf(mx, sv[v]);
+    }
+    mx = xrow_max(mx);
+    const float mn = fmaxf(mrun, mx);  // finite: position 0 is in every row's first tile
+    const float cf = mrun == -INFINITY ? 0.0f : __expf(mrun - mn);
+    float p4[4], ls = 0.0f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      p4[v] = sv[v] == -INFINITY ? 0.0f : __expf(sv[v] - mn);
+      ls += p4[v];
+    }
+    ls = xrow_sum(ls);
+    lrun = lrun * cf + ls;
+    mrun = mn;
+    // O rows are query rows 4kb + v: their factors live in column 4kb + v (lane 4kb + v holds it)
+    float cr[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) cr[v] = __shfl(cf, 4 * kb + v);
+    h4 ph, plo;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const _Float16 hv = (_Float16)p4[v];
+      ph[v] = hv;
+      plo[v] = (_Float16)(p4[v] - (float)hv);
+    }
+    // V rows past the block's last position are zeroed (p is 0 there, but 0 * inf is not)
+    const int nvalid = min(16, last + 1 - ts);
+    const unsigned keep0 = (4 * kb + 0 < nvalid ? 0x0000ffffu : 0u) | (4 * kb + 1 < nvalid ? 0xffff0000u : 0u);
+    const unsigned keep1 = (4 * kb + 2 < nvalid ? 0x0000ffffu : 0u) | (4 * kb + 3 < nvalid ? 0xffff0000u : 0u);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) O[b][v] *= cr[v];
+      const uint2 w = make_uint2(vw[b].x & keep0, vw[b].y & keep1);
+      const h4 vb = __builtin_bit_cast(h4, w);
+      O[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, vb, O[b], 0, 0, 0);
+      O[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(plo, vb, O[b], 0, 0, 0);
+    }
+    if (ts + 16 <= last) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) kw[c] = kn[c];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) vw[b] = vn[b];
+    }
+  }
+  // O[b][v]: query row t0 + 4kb + v, dim 16b + hh; divided by that row's l (column 4kb + v)
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const float l = __shfl(lrun, 4 * kb + v);
+    const int t = t0 + 4 * kb + v;
+    if (t >= T) continue;
+    const size_t ob = (size_t)t * m.q_dim + (size_t)h * HD;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) put_split(Oh, Ol, ob + 16 * b + hh, O[b][v] / l);
   }
 }
 
@@ -477,7 +528,8 @@ hipError_t launch_rope_kv_rows(const ModelDev &m, int layer, float *QKV, int p0,
 
 hipError_t launch_attn_rows(const ModelDev &m, int layer, const float *QKV, int p0, int T, _Float16 *Oh, _Float16 *Ol,
                             hipStream_t s) {
-  const int grid = (T * m.n_heads + 3) / 4;
+  const int waves = (T + 15) / 16 * m.n_heads;  // one wave per (16 rows, query head)
+  const int grid = (waves + PBS / GL3_WAVE - 1) / (PBS / GL3_WAVE);
 #define GL3_AR(HD_)                                                                                          \
   if (m.hd == HD_) {                                                                                         \
     hipLaunchKernelGGL((attn_rows_kernel<HD_>), dim3(grid), dim3(PBS), 0, s, m, layer, QKV, p0, T, Oh, Ol); \
