@@ -990,6 +990,9 @@ extern "C" int gl3_generate_sampled(gl3_plan *p, const int32_t *prompt, int32_t 
   for (int i = 0; i < n_gen; ++i)
     if (!(coins[i] >= 0.0f && coins[i] < 1.0f))
       return fail(GL3_ERR_INVALID_ARGUMENT, "draw %d = %g is not in [0, 1)", i, (double)coins[i]);
+  // temperature 0 is the argmax (Sampler.TENSOR_ARGMAX, Sampler.java:76-78): the
+  // greedy loop, whose steps run up to 256 to a launch with the argmax in the kernel
+  if (temperature == 0.0f) return gl3_generate_from_prompt(p, prompt, n_prompt, position, n_gen, tokens_out);
   int rc = gl3_prepare(p);
   if (rc) return rc;
   HIP_TRY(hipMemcpyAsync((void *)p->m.prompt, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, p->stream));
