@@ -16,7 +16,16 @@ struct StepKernel {
 };
 
 int gemv_n(int fmt, int K);
+// a GEMV of this row length runs: on the compiled GemvPhase tiles, else on the any-length kernel
 bool gemv_supported(int fmt, int K);
+bool gemv_fast(int fmt, int K);  // the compiled tiles (and the persistent kernel's shapes) cover it
+
+// GEMV for any row length (gl3_gemv_any.hip): K a multiple of 32 (Q8_0) or 8 (F16), up to this
+#define GL3_GEMV_ANY_MAX_K 15872
+bool gemv_any_supported(int fmt, int K);
+hipError_t launch_gemv_any(int fmt, int mode, const Mat &W, int out_rows, const float *x, const float *normw,
+                           float eps, float *y, unsigned long long *best, int grid, hipStream_t s);
+hipError_t launch_logits_any(const ModelDev &m, int grid, hipStream_t s);
 hipError_t launch_gemv(int fmt, int mode, const Mat &W, int out_rows, const float *x, const float *normw, float eps,
                        float *y, unsigned long long *best, int grid, hipStream_t s);
 hipError_t launch_logits(const ModelDev &m, int grid, hipStream_t s);

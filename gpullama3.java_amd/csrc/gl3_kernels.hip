@@ -69,13 +69,15 @@ int gemv_n(int fmt, int K) {
   return (K % per == 0) ? K / per : -1;
 }
 
-bool gemv_supported(int fmt, int K) {
+bool gemv_fast(int fmt, int K) {
   const int n = gemv_n(fmt, K);
 #define GL3_SUP(F, N, KC, KS) if (fmt == F && n == N) return true;
   GL3_GEMV_LIST(GL3_SUP)
 #undef GL3_SUP
   return false;
 }
+
+bool gemv_supported(int fmt, int K) { return gemv_fast(fmt, K) || gemv_any_supported(fmt, K); }
 
 hipError_t launch_gemv(int fmt, int mode, const Mat &W, int out_rows, const float *x, const float *normw, float eps,
                        float *y, unsigned long long *best, int grid, hipStream_t s) {
@@ -99,7 +101,8 @@ hipError_t launch_gemv(int fmt, int mode, const Mat &W, int out_rows, const floa
   }
   GL3_GEMV_LIST(GL3_DISPATCH)
 #undef GL3_DISPATCH
-  return hipErrorInvalidValue;
+  // a width outside the compiled tiles
+  return launch_gemv_any(fmt, mode, W, out_rows, x, normw, eps, y, best, grid, s);
 }
 
 template <class P>
@@ -121,7 +124,7 @@ hipError_t launch_logits(const ModelDev &m, int grid, hipStream_t s) {
   }
   GL3_GEMV_LIST(GL3_LOGITS)
 #undef GL3_LOGITS
-  return hipErrorInvalidValue;
+  return launch_logits_any(m, grid, s);  // a width outside the compiled tiles
 }
 
 // ------------------------------------------------------ per-phase kernels
@@ -173,14 +176,14 @@ hipError_t launch_attention(const ModelDev &m, int layer, hipStream_t s) {
     hipLaunchKernelGGL((attention_kernel<HD_, G_>), dim3(grid), dim3(GL3_STEP_BLOCK), lds, s, m, layer);        \
     return hipGetLastError();                                                                                   \
   }
-  GL3_ATT(64, 1) GL3_ATT(64, 2) GL3_ATT(64, 4) GL3_ATT(64, 8)
-  GL3_ATT(96, 1) GL3_ATT(96, 2) GL3_ATT(96, 4) GL3_ATT(96, 8)
-  GL3_ATT(128, 1) GL3_ATT(128, 2) GL3_ATT(128, 4) GL3_ATT(128, 8)
+  GL3_ATT(64, 1) GL3_ATT(64, 2) GL3_ATT(64, 3) GL3_ATT(64, 4) GL3_ATT(64, 8)
+  GL3_ATT(96, 1) GL3_ATT(96, 2) GL3_ATT(96, 3) GL3_ATT(96, 4) GL3_ATT(96, 8)
+  GL3_ATT(128, 1) GL3_ATT(128, 2) GL3_ATT(128, 3) GL3_ATT(128, 4) GL3_ATT(128, 8)
 #undef GL3_ATT
   return hipErrorInvalidValue;
 }
 bool attention_supported(int hd, int G) {
-  return (hd == 64 || hd == 96 || hd == 128) && (G == 1 || G == 2 || G == 4 || G == 8);
+  return (hd == 64 || hd == 96 || hd == 128) && (G == 1 || G == 2 || G == 3 || G == 4 || G == 8);
 }
 hipError_t launch_advance(const ModelDev &m, hipStream_t s) {
   hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(GL3_BLOCK), 0, s, m);

@@ -255,7 +255,7 @@ static int validate_config(const gl3_config *c, int *family) {
     return fail(GL3_ERR_INVALID_ARGUMENT, "head_dim * n_heads must equal dim for this model type");
   const int G = c->n_heads / c->n_kv_heads;
   if (!attention_supported(c->head_dim, G))
-    return fail(GL3_ERR_UNSUPPORTED, "head_dim %d (multiple of 8, <= 128) / GQA group %d (1, 2, 4 or 8) not supported",
+    return fail(GL3_ERR_UNSUPPORTED, "head_dim %d (64, 96 or 128) / GQA group %d (1, 2, 3, 4 or 8) not supported",
                 c->head_dim, G);
   if (!(c->rms_norm_eps > 0.0f) || !(c->rope_theta > 0.0f)) return fail(GL3_ERR_INVALID_ARGUMENT, "eps/theta");
   const int fmt = ggml_to_fmt(c->weight_type);

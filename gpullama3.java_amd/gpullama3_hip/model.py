@@ -62,6 +62,12 @@ CONFIGS = {
                                 F16, F16, False, "Phi-3-mini (synthetic)"),
     "llama8b_q8": ModelShape("llama", 4096, 14336, 32, 32, 8, 128, 128256, 32768 + 128, 1e-5, 500000.0,
                              Q8_0, F16, False, "Llama 3.1 8B (synthetic)"),
+    # shapes on the per-phase schedule (no compiled persistent kernel): GQA group 3,
+    # and row lengths outside the compiled GEMV tiles (dim 2560, hidden 9728)
+    "llama3b_q8": ModelShape("llama", 3072, 8192, 28, 24, 8, 128, 128256, 4096, 1e-5, 500000.0,
+                             Q8_0, F16, False, "Llama 3.2 3B (synthetic)"),
+    "qwen3_4b_f16": ModelShape("qwen3", 2560, 9728, 36, 32, 8, 128, 151936, 4096, 1e-6, 1000000.0,
+                               F16, F16, False, "Qwen3 4B (synthetic)"),
 }
 
 

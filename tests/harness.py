@@ -13,6 +13,8 @@ LAYER_SHAPES = {
     "qwen3_06b_q8": CONFIGS["qwen3_06b_q8"],
     "phi3_mini_f16": CONFIGS["phi3_mini_f16"],
     "llama8b_q8": CONFIGS["llama8b_q8"],
+    "llama3b_q8": CONFIGS["llama3b_q8"],
+    "qwen3_4b_f16": CONFIGS["qwen3_4b_f16"],
 }
 
 

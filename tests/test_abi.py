@@ -60,7 +60,7 @@ def create(cfg):
     (dict(head_dim=72), L.ERR_INVALID_ARGUMENT),           # head_dim * n_heads != dim for Llama
     (dict(context_length=0), L.ERR_INVALID_ARGUMENT),
     (dict(dim=2000, n_heads=20, n_kv_heads=4, head_dim=100), L.ERR_UNSUPPORTED),
-    (dict(dim=1600, n_heads=25, n_kv_heads=5, head_dim=64), L.ERR_UNSUPPORTED),  # GEMV K=1600
+    (dict(dim=1600, n_heads=25, n_kv_heads=5, head_dim=64), L.ERR_UNSUPPORTED),  # GQA group 5
 ])
 def test_invalid_configs_rejected_without_device(mutate, status):
     cfg = gl3_config(CONFIGS["llama1b_q8"])

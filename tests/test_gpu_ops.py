@@ -32,7 +32,8 @@ def test_q8_0_dequant_bit_exact_exhaustive(gpu):
 
 
 GEMV_COLS = [(Q8_0, c) for c in (1024, 2048, 3072, 4096, 8192, 14336)] + \
-            [(F16, c) for c in (1024, 2048, 3072, 4096, 8192, 14336)]
+            [(F16, c) for c in (1024, 2048, 3072, 4096, 8192, 14336)] + \
+            [(t, c) for t in (Q8_0, F16) for c in (1056, 2560, 9728)]  # widths of the any-length kernel
 
 
 def make_w(t, rows, cols, seed):
@@ -75,9 +76,10 @@ def test_gemv_vs_oracle(gpu, t, cols, mode):
 
 
 def test_gemv_rejects_unsupported_width(gpu):
-    w = make_w(Q8_0, 4, 1056, 1)
+    # past the any-length kernel's staging (15,872) and not a compiled tile width
+    w = make_w(Q8_0, 4, 16384 + 1024, 1)
     with pytest.raises(NotImplementedError):
-        P.op_gemv(Q8_0, w, 4, 1056, np.zeros(1056, np.float32))
+        P.op_gemv(Q8_0, w, 4, 16384 + 1024, np.zeros(16384 + 1024, np.float32))
 
 
 def check_attention(hd, n_heads, n_kv, pos, seed):
@@ -96,9 +98,9 @@ def check_attention(hd, n_heads, n_kv, pos, seed):
         assert np.max(np.abs(got[h * hd:(h + 1) * hd] - ref)) <= 2e-5 * np.abs(vc).max().astype(np.float32), h
 
 
-# (head_dim, query heads, kv heads): GQA groups 4, 2, 1 (MHA), 4 and 8
+# (head_dim, query heads, kv heads): GQA groups 4, 2, 1 (MHA), 4, 8 and 3 (Llama-3.2-3B)
 @pytest.mark.parametrize("hd,n_heads,n_kv", [(64, 32, 8), (128, 16, 8), (96, 32, 32), (128, 32, 8), (64, 8, 8),
-                                             (128, 32, 4), (64, 32, 4)])
+                                             (128, 32, 4), (64, 32, 4), (128, 24, 8)])
 @pytest.mark.parametrize("pos", [0, 1, 63, 64, 200, 1500, 4095])
 def test_attention_vs_oracle(gpu, hd, n_heads, n_kv, pos):
     check_attention(hd, n_heads, n_kv, pos, hd * 7919 + pos + 31 * n_kv)

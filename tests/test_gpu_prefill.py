@@ -47,7 +47,8 @@ def teacher_forced(plan, ref, tok, pos, n, tol=TOL_TIGHT):
     return worst
 
 
-@pytest.mark.parametrize("key", ["llama1b_q8", "llama1b_f16", "qwen3_06b_q8", "phi3_mini_f16", "llama8b_q8"])
+@pytest.mark.parametrize("key", ["llama1b_q8", "llama1b_f16", "qwen3_06b_q8", "phi3_mini_f16", "llama8b_q8",
+                                 "llama3b_q8", "qwen3_4b_f16"])
 def test_prefill_matches_oracle(gpu, key):
     """A ragged 77-token prompt: 76 tokens batched, then the last one and 4 greedy steps decoded."""
     shape = small(key, ctx=256)
