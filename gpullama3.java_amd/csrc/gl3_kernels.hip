@@ -228,6 +228,7 @@ typedef Shape<FMT_F16, 2048, 2048,  512,  8192,  64, 4, 8, 3, Tile<4, 1, 3>, Til
 typedef Shape<FMT_Q8,  1024, 2048, 1024,  3072, 128, 2, 8, 3, Tile<1, 1, 4>, Tile<1, 2, 2>, Tile<1, 1, 3>, Tile<3, 1, 1>, Tile<1, 1, 8>> ShapeQwen3_06BQ8;
 typedef Shape<FMT_F16, 3072, 3072, 3072,  8192,  96, 1, 8, 3, Tile<6, 1, 1>, Tile<6, 1, 1>, Tile<3, 2, 1>, Tile<4, 4, 2>, Tile<6, 1, 1>> ShapePhi3MiniF16;
 typedef Shape<FMT_Q8,  4096, 4096, 1024, 14336, 128, 4, 8, 2, Tile<4, 1, 2>, Tile<4, 1, 2>, Tile<4, 1, 1>, Tile<7, 2, 1>, Tile<4, 1, 2>> ShapeLlama8BQ8;
+typedef Shape<FMT_Q8,  3072, 3072, 1024,  8192, 128, 3, 8, 2, Tile<3, 1, 2>, Tile<3, 1, 2>, Tile<3, 1, 1>, Tile<4, 2, 1>, Tile<3, 1, 2>> ShapeLlama3BQ8;
 
 // The first slot-load of the fused FFN's Wdown slice, requested into ring slot
 // 2 (unused by the gate/up phase) once gate/up's last weight slot has arrived,
@@ -400,6 +401,7 @@ bool find_step_kernel(const ModelDev &m, int grid, StepKernel *out) {
   if (shape_matches<ShapeQwen3_06BQ8>(m)) { *out = make_step_kernel<ShapeQwen3_06BQ8>(m, grid); return true; }
   if (shape_matches<ShapePhi3MiniF16>(m)) { *out = make_step_kernel<ShapePhi3MiniF16>(m, grid); return true; }
   if (shape_matches<ShapeLlama8BQ8>(m)) { *out = make_step_kernel<ShapeLlama8BQ8>(m, grid); return true; }
+  if (shape_matches<ShapeLlama3BQ8>(m)) { *out = make_step_kernel<ShapeLlama3BQ8>(m, grid); return true; }
   return false;
 }
 
