@@ -229,6 +229,8 @@ typedef Shape<FMT_Q8,  1024, 2048, 1024,  3072, 128, 2, 8, 3, Tile<1, 1, 4>, Til
 typedef Shape<FMT_F16, 3072, 3072, 3072,  8192,  96, 1, 8, 3, Tile<6, 1, 1>, Tile<6, 1, 1>, Tile<3, 2, 1>, Tile<4, 4, 2>, Tile<6, 1, 1>> ShapePhi3MiniF16;
 typedef Shape<FMT_Q8,  4096, 4096, 1024, 14336, 128, 4, 8, 2, Tile<4, 1, 2>, Tile<4, 1, 2>, Tile<4, 1, 1>, Tile<7, 2, 1>, Tile<4, 1, 2>> ShapeLlama8BQ8;
 typedef Shape<FMT_Q8,  3072, 3072, 1024,  8192, 128, 3, 8, 2, Tile<3, 1, 2>, Tile<3, 1, 2>, Tile<3, 1, 1>, Tile<4, 2, 1>, Tile<3, 1, 2>> ShapeLlama3BQ8;
+typedef Shape<FMT_Q8,  3072, 3072, 3072,  8192,  96, 1, 8, 2, Tile<3, 1, 2>, Tile<3, 1, 2>, Tile<3, 1, 1>, Tile<4, 2, 1>, Tile<3, 1, 2>> ShapePhi3MiniQ8;
+typedef Shape<FMT_F16, 4096, 4096, 1024, 14336, 128, 4, 8, 3, Tile<8, 1, 1>, Tile<8, 1, 1>, Tile<4, 2, 1>, Tile<7, 4, 1>, Tile<8, 1, 1>> ShapeMistral7BF16;
 
 // The first slot-load of the fused FFN's Wdown slice, requested into ring slot
 // 2 (unused by the gate/up phase) once gate/up's last weight slot has arrived,
@@ -402,6 +404,8 @@ bool find_step_kernel(const ModelDev &m, int grid, StepKernel *out) {
   if (shape_matches<ShapePhi3MiniF16>(m)) { *out = make_step_kernel<ShapePhi3MiniF16>(m, grid); return true; }
   if (shape_matches<ShapeLlama8BQ8>(m)) { *out = make_step_kernel<ShapeLlama8BQ8>(m, grid); return true; }
   if (shape_matches<ShapeLlama3BQ8>(m)) { *out = make_step_kernel<ShapeLlama3BQ8>(m, grid); return true; }
+  if (shape_matches<ShapePhi3MiniQ8>(m)) { *out = make_step_kernel<ShapePhi3MiniQ8>(m, grid); return true; }
+  if (shape_matches<ShapeMistral7BF16>(m)) { *out = make_step_kernel<ShapeMistral7BF16>(m, grid); return true; }
   return false;
 }
 

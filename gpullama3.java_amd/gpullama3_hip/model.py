@@ -68,6 +68,11 @@ CONFIGS = {
                              Q8_0, F16, False, "Llama 3.2 3B (synthetic)"),
     "qwen3_4b_f16": ModelShape("qwen3", 2560, 9728, 36, 32, 8, 128, 151936, 4096, 1e-6, 1000000.0,
                                F16, F16, False, "Qwen3 4B (synthetic)"),
+    # the other shapes of the reference's CI runs (build-and-run.yml)
+    "phi3_mini_q8": ModelShape("phi3", 3072, 8192, 32, 32, 32, 96, 32064, 4096, 1e-5, 10000.0,
+                               Q8_0, F16, False, "Phi-3-mini Q8_0 (synthetic)"),
+    "mistral7b_f16": ModelShape("llama", 4096, 14336, 32, 32, 8, 128, 32768, 4096, 1e-5, 1000000.0,
+                                F16, F16, False, "Mistral 7B v0.3 (synthetic)"),
 }
 
 

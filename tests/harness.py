@@ -15,6 +15,8 @@ LAYER_SHAPES = {
     "llama8b_q8": CONFIGS["llama8b_q8"],
     "llama3b_q8": CONFIGS["llama3b_q8"],
     "qwen3_4b_f16": CONFIGS["qwen3_4b_f16"],
+    "phi3_mini_q8": CONFIGS["phi3_mini_q8"],
+    "mistral7b_f16": CONFIGS["mistral7b_f16"],
 }
 
 

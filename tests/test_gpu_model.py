@@ -35,7 +35,7 @@ def run_steps(plan, ref, toks, poss):
 
 @pytest.mark.parametrize("sched", sorted(SCHEDULES))
 @pytest.mark.parametrize("key", ["llama1b_q8", "qwen3_06b_q8", "llama1b_f16", "phi3_mini_f16", "llama8b_q8",
-                                 "llama3b_q8", "qwen3_4b_f16"])
+                                 "llama3b_q8", "qwen3_4b_f16", "phi3_mini_q8", "mistral7b_f16"])
 def test_decode_matches_oracle(gpu, key, sched):
     shape = small(key)
     if key == "llama1b_f16":
