@@ -9,6 +9,7 @@
 //  * op kernels for the op-level C-ABI entry points.
 #include "gl3_internal.h"
 
+
 namespace gl3 {
 
 // ------------------------------------------------------------ GEMV tables
@@ -207,7 +208,9 @@ struct Tile {
 };
 // FFN 1: fused FFN (gate/up rows in contiguous runs of 32 per workgroup, each
 // multiplied by its 32-column slice of Wdown, partials reduced by row);
-// needs Q8_0, a two-slot ring, hidden = 32 x grid and dim = R x grid, R <= 8.
+// needs Q8_0, a two-slot ring, hidden = 32 x grid, dim = R x grid, R <= 8, and
+// gate/up tiles such that a workgroup's 32 rows are four slot-loads (held in
+// ring slots 0..3 at once).
 template <int FMT_, int DIM, int QD, int KVD, int HID, int HD, int G, int SC, int DEPTH, class TQKV, class TWO,
           class TGU, class TDN, class TCLS, int FFN = 0>
 struct Shape {
@@ -216,7 +219,8 @@ struct Shape {
   static constexpr int BS = GL3_STEP_BLOCK;
   typedef GemvPhase<FMT_, TQKV::KC, TQKV::KS, TQKV::NR, MODE_STORE, BS, SC, DEPTH> QKV;
   typedef GemvPhase<FMT_, TWO::KC, TWO::KS, TWO::NR, MODE_RESIDUAL, BS, SC, DEPTH> WO;
-  typedef GemvPhase<FMT_, TGU::KC, TGU::KS, TGU::NR, MODE_SWIGLU, BS, SC, DEPTH, FFN> GU;
+  // fused FFN: the four gate/up slot-loads of a workgroup are all requested ahead (ring slots 0..3)
+  typedef GemvPhase<FMT_, TGU::KC, TGU::KS, TGU::NR, MODE_SWIGLU, BS, SC, FFN == 1 ? 4 : DEPTH, FFN> GU;
   typedef DownSliceQ8<BS, DEPTH> DS;
   typedef GemvPhase<FMT_, TDN::KC, TDN::KS, TDN::NR, MODE_RESIDUAL, BS, SC, DEPTH> DOWN;
   typedef GemvPhase<FMT_, TCLS::KC, TCLS::KS, TCLS::NR, MODE_LOGITS, BS, SC, DEPTH> CLS;
@@ -232,14 +236,18 @@ typedef Shape<FMT_Q8,  3072, 3072, 1024,  8192, 128, 3, 8, 2, Tile<3, 1, 2>, Til
 typedef Shape<FMT_Q8,  3072, 3072, 3072,  8192,  96, 1, 8, 2, Tile<3, 1, 2>, Tile<3, 1, 2>, Tile<3, 1, 1>, Tile<4, 2, 1>, Tile<3, 1, 2>> ShapePhi3MiniQ8;
 typedef Shape<FMT_F16, 4096, 4096, 1024, 14336, 128, 4, 8, 3, Tile<8, 1, 1>, Tile<8, 1, 1>, Tile<4, 2, 1>, Tile<7, 4, 1>, Tile<8, 1, 1>> ShapeMistral7BF16;
 
-// The first slot-load of the fused FFN's Wdown slice, requested into ring slot
-// 2 (unused by the gate/up phase) once gate/up's last weight slot has arrived,
-// so it streams while gate/up finishes.
+// The fused FFN's Wdown slice (two slot-loads), requested into ring slots 0
+// and 1 as soon as gate/up's dot products are done with them, so it streams
+// while gate/up finishes.
 template <class DS>
-struct DownSliceFirstHalf {
+struct DownSliceAfterGateUp {
   Mat W;
   int rows, slice;
-  __device__ __forceinline__ void operator()() { DS::template issue<2>(W, rows, slice, 0); }
+  __device__ __forceinline__ void operator()() {}
+  __device__ __forceinline__ void after(int u) {
+    if (u == 0) DS::template issue<0>(W, rows, slice, 0);
+    if (u == 1) DS::template issue<1>(W, rows, slice, 1);
+  }
 };
 
 // n_steps greedy decode steps in one launch: per step embedding, L x (QKV,
@@ -289,30 +297,41 @@ __global__ __launch_bounds__(GL3_STEP_BLOCK, 1) void decode_step_kernel(ModelDev
                                                                   m.tstamp ? tk : -1);
       tk += 2;
       trace(m, tk++);
+      // workgroups without an attention item wait quietly for the attention output
+      const int msplit = max(1, min(min(m.max_split, 64), nblk / m.n_kv));
+      const int S = att_split_len(si.pos + 1, msplit, 16 * (SH::BS / GL3_WAVE));
+      const bool att_wg = blk < m.n_kv * ((si.pos + S) / S);
       SH::WO::prefetch(ld_mat(&L->wo), SH::dim, blk, nblk);
-      {
-        // workgroups without an attention item wait quietly for the attention output
-        const int msplit = max(1, min(min(m.max_split, 64), nblk / m.n_kv));
-        const int S = att_split_len(si.pos + 1, msplit, 16 * (SH::BS / GL3_WAVE));
-        if (blk >= m.n_kv * ((si.pos + S) / S))
-          quiet_wait(m.tatt, SH::gqa * SH::hd, SH::gqa * SH::hd - 1, m.n_kv, t_att, tw);
-      }
-      SH::WO::run(ld_mat(&L->wo), SH::dim, InTag{m.tatt, t_att, tw}, nullptr, m.eps, OutTag{m.txb, t_wo, m.txa, t_x, tw},
-                  nullptr, blk, nblk, lds, true);
-      trace(m, tk++);
-      SH::GU::prefetch(ld_mat(&L->gu), SH::hidden, blk, nblk);
-      trace(m, tk++);
       if constexpr (SH::ffn == 1) {
-        // fused FFN: this workgroup's 32 SwiGLU rows stay in LDS and meet its
-        // 32-column slice of Wdown; t_hb tags the partial sums
+        // fused FFN: gate/up's slot-loads 1..3 go into ring slots 1..3 (free
+        // during Wo) while the workgroup has nothing else to read: before the
+        // wait for the attention output when it holds no attention item, else
+        // once Wo's output is stored; slot-load 0 follows Wo (slot 0 holds Wo)
+        const Mat wgu = ld_mat(&L->gu);
+        if (!att_wg) {
+          SH::GU::template issue<1>(wgu, SH::hidden, 1, blk, nblk);
+          SH::GU::template issue<2>(wgu, SH::hidden, 2, blk, nblk);
+          SH::GU::template issue<3>(wgu, SH::hidden, 3, blk, nblk);
+          quiet_wait(m.tatt, SH::gqa * SH::hd, SH::gqa * SH::hd - 1, m.n_kv, t_att, tw);
+        }
+        SH::WO::run(ld_mat(&L->wo), SH::dim, InTag{m.tatt, t_att, tw}, nullptr, m.eps,
+                    OutTag{m.txb, t_wo, m.txa, t_x, tw}, nullptr, blk, nblk, lds, true);
+        trace(m, tk++);
+        if (att_wg) {
+          SH::GU::template issue<1>(wgu, SH::hidden, 1, blk, nblk);
+          SH::GU::template issue<2>(wgu, SH::hidden, 2, blk, nblk);
+          SH::GU::template issue<3>(wgu, SH::hidden, 3, blk, nblk);
+        }
+        SH::GU::template issue<0>(wgu, SH::hidden, 0, blk, nblk);
+        trace(m, tk++);
+        // this workgroup's 32 SwiGLU rows stay in LDS and meet its 32-column
+        // slice of Wdown; t_hb tags the partial sums
         const Mat wds = ld_mat(&L->down_sl);
-        SH::GU::run(ld_mat(&L->gu), SH::hidden, InTag{m.txb, t_wo, tw}, L->ffn_norm, m.eps, OutNone{}, nullptr, blk,
-                    nblk, lds, true, DownSliceFirstHalf<typename SH::DS>{wds, SH::dim, blk});
-        // the first half went out with gate/up's last slot (every workgroup holds gate/up items)
+        SH::GU::run(wgu, SH::hidden, InTag{m.txb, t_wo, tw}, L->ffn_norm, m.eps, OutNone{}, nullptr, blk, nblk, lds,
+                    true, DownSliceAfterGateUp<typename SH::DS>{wds, SH::dim, blk});
         trace(m, tk++);
-        SH::DS::template issue<0>(wds, SH::dim, blk, 1);
         trace(m, tk++);
-        SH::DS::template run<2, 0>(SH::dim, lds + SH::GU::obuf_offset(SH::dim, true), m.tdp + (size_t)blk * SH::dim,
+        SH::DS::template run<0, 1>(SH::dim, lds + SH::GU::obuf_offset(SH::dim, true), m.tdp + (size_t)blk * SH::dim,
                                    t_hb);
         trace(m, tk++);
         // the reduce polls the partials first: weight requests issued before them
@@ -325,6 +344,12 @@ __global__ __launch_bounds__(GL3_STEP_BLOCK, 1) void decode_step_kernel(ModelDev
           SH::CLS::prefetch(m.cls, m.vocab, blk, nblk);
         trace(m, tk++);
       } else {
+        if (!att_wg) quiet_wait(m.tatt, SH::gqa * SH::hd, SH::gqa * SH::hd - 1, m.n_kv, t_att, tw);
+        SH::WO::run(ld_mat(&L->wo), SH::dim, InTag{m.tatt, t_att, tw}, nullptr, m.eps,
+                    OutTag{m.txb, t_wo, m.txa, t_x, tw}, nullptr, blk, nblk, lds, true);
+        trace(m, tk++);
+        SH::GU::prefetch(ld_mat(&L->gu), SH::hidden, blk, nblk);
+        trace(m, tk++);
         SH::GU::run(ld_mat(&L->gu), SH::hidden, InTag{m.txb, t_wo, tw}, L->ffn_norm, m.eps,
                     OutTag{m.thb, t_hb, nullptr, 0u, tw}, nullptr, blk, nblk, lds, true);
         trace(m, tk++);
@@ -391,7 +416,8 @@ static StepKernel make_step_kernel(const ModelDev &m, int grid) {
     // one 32-column slice of Wdown per workgroup: the grid is fixed
     k.req_grid = SH::hidden / 32;
     const bool ok = SH::GU::items(SH::hidden) % k.req_grid == 0 && SH::dim % k.req_grid == 0 &&
-                    SH::dim / k.req_grid <= 8 && SH::dim % (2 * SH::DS::RPU) == 0 && SH::dim == 2 * SH::DS::RPU;
+                    SH::dim / k.req_grid <= 8 && SH::dim % (2 * SH::DS::RPU) == 0 && SH::dim == 2 * SH::DS::RPU &&
+                    SH::GU::local_items(SH::hidden, 0, k.req_grid) * SH::GU::PASSES == 4;
     if (!ok || k.req_grid > k.max_grid) k.req_grid = -1;  // this shape cannot run fused
   }
   return k;

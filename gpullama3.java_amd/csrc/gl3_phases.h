@@ -523,14 +523,21 @@ __device__ __forceinline__ void dma4(dma_rsrc_t r, void *lds, unsigned voff, uns
 }
 
 // Loads a GEMV phase may request for the phase after it once its own last
-// slot has arrived (so they do not delay its waits): called at most once, after
-// the wait for the last slot and before that slot's dot products.
+// slot has arrived (so they do not delay its waits): operator() is called at
+// most once, after the wait for the last slot and before that slot's dot
+// products; after(u) after the dot products of slot-load u (its ring slot may
+// then take other loads).
 struct NoTail {
   __device__ __forceinline__ void operator()() {}
+  __device__ __forceinline__ void after(int) {}
 };
 
 // MAP 0: workgroup blk takes items blk, blk + nblk, ...; MAP 1: the items are
 // split into nblk contiguous runs (the host checks that nblk divides them).
+// DEPTH 4: the workgroup's slot-loads 0..3 sit in ring slots 0..3 and are all
+// issued before run() (in any order, at any time the slots are free); run()
+// reads them once its input is staged, which waits for every load issued
+// before it.  Further slot-loads (u >= 4) reuse the slots with full waits.
 template <int FMT, int KC, int KS, int NR, int MODE, int BS, int SC_ = 0, int DEPTH = 2, int MAP = 0>
 struct GemvPhase {
   typedef ChunkTraits<FMT> T;
@@ -552,7 +559,7 @@ struct GemvPhase {
   static constexpr int NI_MIN = NR * NP * JMIN + NSI;    // fewest loads a slot takes
   static_assert(WPB % KS == 0, "K-split must divide the waves of a workgroup");
   static_assert(SC % 4 == 0 && NR * NP <= SC && JP >= 1, "ring slot too small for the rows of a wave");
-  static_assert(DEPTH == 2 || DEPTH == 3, "ring depth");
+  static_assert(DEPTH >= 2 && DEPTH <= 4, "ring depth");
   // x of the lane lives in registers when an item is one slot load and the
   // slice is at most 128 floats; when no norm applies and no two waves share a
   // slice, each wave loads its slice itself (no LDS staging).
@@ -628,7 +635,8 @@ struct GemvPhase {
     const int nu = local_items(out_rows, blk, nblk) * PASSES;
     if (nu > 0) issue<0>(W, out_rows, 0, blk, nblk);
     if (nu > 1) issue<1>(W, out_rows, 1, blk, nblk);
-    if (DEPTH == 3 && nu > 2) issue<(DEPTH == 3 ? 2 : 1)>(W, out_rows, 2, blk, nblk);
+    if (DEPTH >= 3 && nu > 2) issue<(DEPTH >= 3 ? 2 : 1)>(W, out_rows, 2, blk, nblk);
+    if (DEPTH == 4 && nu > 3) issue<(DEPTH == 4 ? 3 : 1)>(W, out_rows, 3, blk, nblk);
   }
 
   struct XSlice {
@@ -729,7 +737,11 @@ struct GemvPhase {
     if (u < nu) {
       // slot S is complete once at most the loads of the (up to DEPTH-1) later slot-loads are outstanding
       const int later = nu - 1 - u;
-      if (DEPTH == 3 && later >= 2)
+      if (DEPTH == 4) {
+        // slot-loads 0..3 completed before the input was staged; later ones are waited for in full
+        if (u >= DEPTH) wait_vmem<0>();
+        if (later == 0) tail();
+      } else if (DEPTH == 3 && later >= 2)
         wait_vmem<2 * NI_MIN>();
       else if (later >= 1)
         wait_vmem<NI_MIN>();
@@ -739,6 +751,7 @@ struct GemvPhase {
       }
       const int pass = PASSES > 1 ? u % PASSES : 0;
       dot_slot<S>(xr, pass, acc);
+      tail.after(u);
       if (u + DEPTH < nu) issue<S>(W, out_rows, u + DEPTH, blk, nblk);
       if (PASSES == 1 || pass == PASSES - 1) {
         finish_item(u / PASSES, acc, kpart, obuf);
@@ -832,6 +845,8 @@ struct GemvPhase {
       }
     }
 
+    // DEPTH 4: the preloaded slots were issued before the input reads, so this wait is already met
+    if (DEPTH == 4) wait_vmem<0>();
     float acc[NR][NP];
 #pragma unroll
     for (int r = 0; r < NR; ++r)
@@ -840,7 +855,8 @@ struct GemvPhase {
     for (int u = 0; u < nu; u += DEPTH) {
       step<0>(W, out_rows, u, nu, blk, nblk, xr, acc, kpart, obuf, tail);
       step<1>(W, out_rows, u + 1, nu, blk, nblk, xr, acc, kpart, obuf, tail);
-      if (DEPTH == 3) step<(DEPTH == 3 ? 2 : 1)>(W, out_rows, u + 2, nu, blk, nblk, xr, acc, kpart, obuf, tail);
+      if (DEPTH >= 3) step<(DEPTH >= 3 ? 2 : 1)>(W, out_rows, u + 2, nu, blk, nblk, xr, acc, kpart, obuf, tail);
+      if (DEPTH == 4) step<(DEPTH == 4 ? 3 : 1)>(W, out_rows, u + 3, nu, blk, nblk, xr, acc, kpart, obuf, tail);
     }
     __syncthreads();
 
