@@ -583,15 +583,37 @@ struct GemvPhase {
     return MAP == 1 ? blk * (items(out_rows) / nblk) + i : blk + i * nblk;
   }
 
+  // Ring slot S (0 <= S < DEPTH) chosen at run time: the step loop is one copy
+  // of code for all slots (a loop body per slot, unrolled, overflows the
+  // instruction cache of the persistent kernel's layer loop).
+  static __device__ __forceinline__ u32x4 *slot_w(int S) {
+    u32x4 *p = ring_w<0, WCH>();
+    if (S == 1) p = ring_w<1, WCH>();
+    if (DEPTH >= 3 && S == 2) p = ring_w<(DEPTH >= 3 ? 2 : 0), WCH>();
+    if (DEPTH == 4 && S == 3) p = ring_w<(DEPTH == 4 ? 3 : 0), WCH>();
+    return p;
+  }
+  static __device__ __forceinline__ unsigned *slot_s(int S) {
+    unsigned *p = ring_s<0, SDW>();
+    if (S == 1) p = ring_s<1, SDW>();
+    if (DEPTH >= 3 && S == 2) p = ring_s<(DEPTH >= 3 ? 2 : 0), SDW>();
+    if (DEPTH == 4 && S == 3) p = ring_s<(DEPTH == 4 ? 3 : 0), SDW>();
+    return p;
+  }
+
   // Issues the loads of slot-load u (the workgroup's item u / PASSES, pass u % PASSES) into ring slot S.
   template <int S>
   static __device__ __forceinline__ void issue(const Mat &W, int out_rows, int u, int blk, int nblk) {
+    issue_at(ring_w<S, WCH>(), ring_s<S, SDW>(), W, out_rows, u, blk, nblk);
+  }
+  static __device__ __forceinline__ void issue_at(u32x4 *ring, unsigned *rings, const Mat &W, int out_rows, int u,
+                                                  int blk, int nblk) {
     const int wave = wave_id(), lane = lane_id();
     const int ks = wave % KS, rg = wave / KS;
     const int K = W.cols;
     const int item = item_of(u / PASSES, out_rows, blk, nblk), pass = PASSES > 1 ? u % PASSES : 0;
     const int j0 = pass * JP;
-    u32x4 *rw = ring_w<S, WCH>() + wave * SC * GL3_WAVE;
+    u32x4 *rw = ring + wave * SC * GL3_WAVE;
     const dma_rsrc_t rq = rsrc(W.q);
     wait_lds();  // reads of the slot's previous contents have completed
 #pragma unroll
@@ -612,7 +634,7 @@ struct GemvPhase {
       // scales: NR*NP segments of SEG bytes (the pass's chunks), 4 bytes per lane per load
       constexpr int TOTAL = NR * NP * SEG;
       const int valid = (PASSES > 1 && KC - j0 < JP) ? (KC - j0) * 64 : SEG;
-      unsigned *rs = ring_s<S, SDW>() + wave * SC * 16;
+      unsigned *rs = rings + wave * SC * 16;
       const dma_rsrc_t rsc = rsrc(W.s);
 #pragma unroll
       for (int i = 0; i < NSI; ++i) {
@@ -648,12 +670,12 @@ struct GemvPhase {
     }
   };
 
-  // acc[r][p] += the lane's part of the dot products held in slot S (pass `pass` of the item)
-  template <int S>
-  static __device__ __forceinline__ void dot_slot(const XSlice &xr, int pass, float (&acc)[NR][NP]) {
+  // acc[r][p] += the lane's part of the dot products held in ring slot (ring, rings) (pass `pass` of the item)
+  static __device__ __forceinline__ void dot_at(const u32x4 *ring, const unsigned *rings, const XSlice &xr, int pass,
+                                                float (&acc)[NR][NP]) {
     const int wave = wave_id(), lane = lane_id();
-    const u32x4 *rw = ring_w<S, WCH>() + wave * SC * GL3_WAVE + lane;
-    const uint8_t *rs = (const uint8_t *)(ring_s<S, SDW>() + wave * SC * 16);
+    const u32x4 *rw = ring + wave * SC * GL3_WAVE + lane;
+    const uint8_t *rs = (const uint8_t *)(rings + wave * SC * 16);
     const int j0 = pass * JP;
 #pragma unroll
     for (int r = 0; r < NR; ++r)
@@ -691,8 +713,10 @@ struct GemvPhase {
   }
 
   // Reduces and combines the K-split partials of the workgroup's i-th item;
-  // the row values go to obuf[i * ROWS_PER_ITEM + row in item].
-  static __device__ __forceinline__ void finish_item(int i, float (&acc)[NR][NP], float *kpart, float *obuf) {
+  // the row values go to obuf[i * ROWS_PER_ITEM + row in item] (MODE_SWIGLU:
+  // the gate there and the up value in ubuf, combined after the last item).
+  static __device__ __forceinline__ void finish_item(int i, float (&acc)[NR][NP], float *kpart, float *obuf,
+                                                     float *ubuf) {
     const int wave = wave_id(), lane = lane_id();
     const int ks = wave % KS, rg = wave / KS;
 #pragma unroll
@@ -726,44 +750,46 @@ struct GemvPhase {
           a0 = acc[r][0];
           a1 = acc[r][NP - 1];
         }
-      obuf[i * ROWS_PER_ITEM + rg * NR + lane] = (MODE == MODE_SWIGLU) ? silu_ref(a0) * a1 : a0;
+      obuf[i * ROWS_PER_ITEM + rg * NR + lane] = a0;
+      if (MODE == MODE_SWIGLU) ubuf[i * ROWS_PER_ITEM + rg * NR + lane] = a1;
     }
   }
 
-  template <int S, class TAIL>
+  template <class TAIL>
   static __device__ __forceinline__ void step(const Mat &W, int out_rows, int u, int nu, int blk, int nblk,
                                               const XSlice &xr, float (&acc)[NR][NP], float *kpart, float *obuf,
-                                              TAIL &tail) {
-    if (u < nu) {
-      // slot S is complete once at most the loads of the (up to DEPTH-1) later slot-loads are outstanding
-      const int later = nu - 1 - u;
-      if (DEPTH == 4) {
-        // slot-loads 0..3 completed before the input was staged; later ones are waited for in full
-        if (u >= DEPTH) wait_vmem<0>();
-        if (later == 0) tail();
-      } else if (DEPTH == 3 && later >= 2)
-        wait_vmem<2 * NI_MIN>();
-      else if (later >= 1)
-        wait_vmem<NI_MIN>();
-      else {
-        wait_vmem<0>();
-        tail();
-      }
-      const int pass = PASSES > 1 ? u % PASSES : 0;
-      dot_slot<S>(xr, pass, acc);
-      tail.after(u);
-      if (u + DEPTH < nu) issue<S>(W, out_rows, u + DEPTH, blk, nblk);
-      if (PASSES == 1 || pass == PASSES - 1) {
-        finish_item(u / PASSES, acc, kpart, obuf);
+                                              float *ubuf, TAIL &tail) {
+    const int S = u % DEPTH;
+    // slot S is complete once at most the loads of the (up to DEPTH-1) later slot-loads are outstanding
+    const int later = nu - 1 - u;
+    if (DEPTH == 4) {
+      // slot-loads 0..3 completed before the input was staged; later ones are waited for in full
+      if (u >= DEPTH) wait_vmem<0>();
+      if (later == 0) tail();
+    } else if (DEPTH == 3 && later >= 2)
+      wait_vmem<2 * NI_MIN>();
+    else if (later >= 1)
+      wait_vmem<NI_MIN>();
+    else {
+      wait_vmem<0>();
+      tail();
+    }
+    const int pass = PASSES > 1 ? u % PASSES : 0;
+    u32x4 *rw = slot_w(S);
+    unsigned *rs = slot_s(S);
+    dot_at(rw, rs, xr, pass, acc);
+    tail.after(u);
+    if (u + DEPTH < nu) issue_at(rw, rs, W, out_rows, u + DEPTH, blk, nblk);
+    if (PASSES == 1 || pass == PASSES - 1) {
+      finish_item(u / PASSES, acc, kpart, obuf, ubuf);
 #pragma unroll
-        for (int r = 0; r < NR; ++r)
+      for (int r = 0; r < NR; ++r)
 #pragma unroll
-          for (int p = 0; p < NP; ++p) acc[r][p] = 0.0f;
-      }
+        for (int p = 0; p < NP; ++p) acc[r][p] = 0.0f;
     }
   }
 
-  // LDS layout of a phase: [x (K floats, when staged)] [red 32] [kpart] [obuf] [best keys]
+  // LDS layout of a phase: [x (K floats, when staged)] [red 32] [kpart] [obuf] [best keys | SwiGLU up values]
   static __host__ __device__ constexpr int kpart_floats() { return RG * NR * NP * KS; }
   // float offset of obuf (the workgroup's row values, in local item order) in the phase's LDS
   static __host__ __device__ __forceinline__ int obuf_offset(int K, bool has_norm) {
@@ -772,7 +798,8 @@ struct GemvPhase {
   static __host__ __device__ __forceinline__ bool staged(bool has_norm) { return !(XDIRECT_OK && !has_norm); }
   static __host__ __device__ __forceinline__ size_t lds_bytes(int K, int out_rows, int nblk, bool has_norm) {
     const int lr = local_items(out_rows, 0, nblk) * ROWS_PER_ITEM;
-    return (size_t)((staged(has_norm) ? K : 0) + 32 + kpart_floats() + lr + 2 * WPB + 4) * sizeof(float);
+    return (size_t)((staged(has_norm) ? K : 0) + 32 + kpart_floats() + (MODE == MODE_SWIGLU ? 2 : 1) * lr + 2 * WPB +
+                    4) * sizeof(float);
   }
 
   // Runs the phase.  x: input vector (K floats, coherent); normw: RMSNorm
@@ -792,6 +819,7 @@ struct GemvPhase {
     float *kpart = red + 32;                  // cross-wave partials
     float *obuf = kpart + kpart_floats();     // row values of the workgroup's items
     const int nli = local_items(out_rows, blk, nblk);
+    float *ubuf = obuf + nli * ROWS_PER_ITEM;  // MODE_SWIGLU: up values of the same rows
     const int nu = nli * PASSES;
     if (!prefetched) prefetch(W, out_rows, blk, nblk);
 
@@ -852,11 +880,17 @@ struct GemvPhase {
     for (int r = 0; r < NR; ++r)
 #pragma unroll
       for (int p = 0; p < NP; ++p) acc[r][p] = 0.0f;
-    for (int u = 0; u < nu; u += DEPTH) {
-      step<0>(W, out_rows, u, nu, blk, nblk, xr, acc, kpart, obuf, tail);
-      step<1>(W, out_rows, u + 1, nu, blk, nblk, xr, acc, kpart, obuf, tail);
-      if (DEPTH >= 3) step<(DEPTH >= 3 ? 2 : 1)>(W, out_rows, u + 2, nu, blk, nblk, xr, acc, kpart, obuf, tail);
-      if (DEPTH == 4) step<(DEPTH == 4 ? 3 : 1)>(W, out_rows, u + 3, nu, blk, nblk, xr, acc, kpart, obuf, tail);
+#pragma unroll 1
+    for (int u = 0; u < nu; ++u) step(W, out_rows, u, nu, blk, nblk, xr, acc, kpart, obuf, ubuf, tail);
+    if (MODE == MODE_SWIGLU && ks == 0) {
+      // silu(gate) * up for the rows this wave finished, one lane per row: the
+      // double-precision exp runs once per wave, not once per item (a lone wave
+      // per SIMD waits out its whole latency each time)
+      const int rg = wave / KS;
+      for (int q = lane; q < nli * NR; q += GL3_WAVE) {
+        const int o = (q / NR) * ROWS_PER_ITEM + rg * NR + q % NR;
+        obuf[o] = silu_ref(obuf[o]) * ubuf[o];
+      }
     }
     __syncthreads();
 
