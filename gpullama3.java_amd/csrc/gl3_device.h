@@ -268,6 +268,20 @@ __device__ __forceinline__ bool tag_retry(const TagWait &tw, unsigned &spins) {
 // first reads are issued before any is checked, then missing cells are polled
 // one float4 at a time (polling all of them at once multiplies the polling
 // traffic, which competes with the weight stream: measured slower).
+//
+// Load side of the cell protocol: each 16-byte load covers two cells and is
+// accepted only when both carry the tag.  What it relies on is that each
+// naturally aligned 8-byte half of the load is observed whole, i.e. never
+// pairs the value of one store with the tag of another.  The 16 bytes lie in
+// one 64-byte line and reach the memory side as one request, while every
+// write to a cell is one aligned 8-byte store; a torn half would need the
+// 16-byte read to be split below 8-byte granularity and interleaved with a
+// store, which the cache hierarchy (line-granular requests) does not do.  This
+// is an observed hardware property, not one the programming model states for
+// loads wider than 8 bytes; the per-token parity tests (every cell of every
+// exchanged vector, thousands of tokens per run) would show a torn read as a
+// wrong value, and ld_tagged1 (one 8-byte atomic load per cell) is the drop-in
+// replacement if a target ever breaks it.
 template <int N>
 __device__ __forceinline__ void ld_tagged4(const uint2 *p, const int (&e)[N], unsigned tag, const TagWait &tw,
                                            float4 (&v)[N]) {
