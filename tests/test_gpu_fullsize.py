@@ -19,6 +19,12 @@ differently cannot make the sequences drift apart.
 * Llama-3.1-8B Q8_0: 4 steps from each KV fill 8192, 16384 and 32768 over an
   fp16 N(0,1) history (32 full-size layers; 16 and 32 attention splits of 1024
   positions per kv head at the two longer fills).
+* The other models of the reference's CI runs, at full size: Llama-3.2-3B Q8_0
+  (GQA group 3), Phi-3-mini Q8_0 and Mistral-7B FP16 (persistent kernel) and
+  Qwen3-4B FP16 (per-phase schedule, GEMV widths 2560 / 9728): a 64-token
+  prompt through the batched prefill over an fp16 N(0,1) history of 3000
+  positions (K and V checked at every new position and layer), then 16 greedy
+  steps.
 """
 import os
 import time
@@ -151,3 +157,10 @@ def test_llama8b_kv_fills(gpu):
     assert total > 0
     plan.free_execution_plan()
     ref.close()
+
+
+@pytest.mark.parametrize("key", ["llama3b_q8", "phi3_mini_q8", "mistral7b_f16", "qwen3_4b_f16"])
+def test_ci_models_prefill_then_greedy(gpu, key):
+    shape = CONFIGS[key].with_(context_length=3200)
+    prompt = np.random.default_rng(11).integers(0, shape.vocab_size, 64)
+    assert run(shape, prompt, 16, start=3000, prefill=True) > 0
