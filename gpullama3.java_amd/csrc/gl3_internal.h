@@ -56,7 +56,7 @@ hipError_t launch_fill_normal_vt(uint16_t *vt, int hd, int npos, unsigned long l
 
 // batched prefill (gl3_prefill.hip)
 bool prefill_supported(const ModelDev &m);
-#define GL3_PREFILL_PART_FLOATS ((size_t)768 * 64 * 128)  // split-K partials of one prefill matrix product
+#define GL3_PREFILL_PART_FLOATS ((size_t)1280 * 64 * 128)  // split-K partials of one prefill matrix product
 hipError_t launch_prefill_gemm(int fmt, int mode, const Mat &W, int N, const _Float16 *Xh, const _Float16 *Xl, int T,
                                float *Y, _Float16 *Yh, _Float16 *Yl, float *part, hipStream_t s);
 hipError_t launch_embed_rows(const ModelDev &m, const int *tokens, int T, float *X, hipStream_t s);
