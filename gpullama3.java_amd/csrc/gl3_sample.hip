@@ -5,8 +5,9 @@
 // rng.nextFloat(1f).
 //
 // One workgroup of 1024 threads.  Probabilities follow the reference's float
-// arithmetic (logit / temperature, max, exp in double rounded to float, divide
-// by the sum) except that the sum of the exponentials is the float nearest
+// arithmetic (logit / temperature, max, exp, divide by the sum) with two
+// deviations: exp is the float expf (the reference rounds a double exp to
+// float; the two differ by an ulp or two), and the sum of the exponentials is the float nearest
 // their exact sum (the reference's float sum in index order drifts by up to
 // ~1e-4 relative over a 128k vocabulary); the cumulative sums the samplers
 // compare with the draw and with topp are exact: every probability is converted to a 48-bit fixed-point
