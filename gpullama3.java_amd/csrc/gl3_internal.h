@@ -42,8 +42,11 @@ hipError_t launch_slice_q8(const uint8_t *q, const uint16_t *s, int rows, int co
 hipError_t launch_step_kernel(const StepKernel &k, const ModelDev &m, const GridBarrier &gb, unsigned epoch,
                               unsigned tag, int grid, int n_steps, hipStream_t s);
 
+// probs: scratch of 2 n floats (the probabilities, then the top-p candidates' indices);
+// best (nullable, with st): the decode step's argmax keys, which give the maximum logit
 hipError_t launch_sample(const float *logits, int n, float temperature, float topp, const float *coins, int coin_index,
-                         float *probs, int *token_out, DecodeState *st, int *rec, hipStream_t s);
+                         float *probs, int *token_out, DecodeState *st, int *rec, const unsigned long long *best,
+                         hipStream_t s);
 hipError_t launch_repack_q8(const uint8_t *blocks, size_t nblocks, uint8_t *q, uint16_t *s, hipStream_t st);
 hipError_t launch_dequant_q8(const uint8_t *q, const uint16_t *s, size_t n, float *out, hipStream_t st);
 hipError_t launch_f16_to_f32(const uint16_t *in, size_t n, float *out, hipStream_t st);

@@ -113,7 +113,7 @@ struct gl3_plan {
   // attention output, b: SwiGLU output)
   float *pf_x = nullptr, *pf_qkv = nullptr, *pf_part = nullptr;
   _Float16 *pf_ah = nullptr, *pf_al = nullptr, *pf_bh = nullptr, *pf_bl = nullptr;
-  float *probs = nullptr;             // sampler scratch [vocab]
+  float *probs = nullptr;             // sampler scratch [2 vocab]: probabilities, then candidate indices
   float *coins = nullptr;             // sampler draws of the current generate call [context length]
   DecodeState *h_state = nullptr;     // pinned
   unsigned long long *h_best = nullptr;  // pinned [nbest]
@@ -372,7 +372,7 @@ extern "C" int gl3_create(const gl3_config *cfg, gl3_plan **out) {
   TRY(dev_alloc(p, &m.best, 2 * (size_t)p->nbest));
   TRY(dev_alloc(p, &m.st, 1));
   TRY(dev_alloc(p, &m.tokens_out, (size_t)cfg->context_length));
-  TRY(dev_alloc(p, &p->probs, (size_t)cfg->vocab_size));
+  TRY(dev_alloc(p, &p->probs, 2 * (size_t)cfg->vocab_size));
   TRY(dev_alloc(p, &p->coins, (size_t)cfg->context_length));
   {
     int *pr = nullptr;
@@ -1004,7 +1004,7 @@ extern "C" int gl3_generate_sampled(gl3_plan *p, const int32_t *prompt, int32_t 
   for (int k = 0; k < n_gen; ++k) {
     if ((rc = launch_steps(p, 1))) return rc;
     HIP_TRY(launch_sample(p->m.logits, p->cfg.vocab_size, temperature, topp, p->coins, k, p->probs, nullptr, p->m.st,
-                          p->m.tokens_out, p->stream));
+                          p->m.tokens_out, p->m.best, p->stream));
   }
   if ((rc = end_steps(p))) return rc;
   HIP_TRY(hipMemcpyAsync(tokens_out, p->m.tokens_out, (size_t)n_gen * 4, hipMemcpyDeviceToHost, p->stream));
@@ -1245,14 +1245,14 @@ extern "C" int gl3_op_sample(const float *logits, int32_t n, float temperature, 
       return fail(GL3_ERR_INVALID_ARGUMENT, "draw %d = %g is not in [0, 1)", i, (double)coins[i]);
   DevBuf dl, dp, dc, dt;
   DEV_ALLOC(dl, (size_t)n * 4);
-  DEV_ALLOC(dp, (size_t)n * 4);
+  DEV_ALLOC(dp, 2 * (size_t)n * 4);  // probabilities, then candidate indices
   DEV_ALLOC(dc, (size_t)n_draws * 4);
   DEV_ALLOC(dt, (size_t)n_draws * 4);
   HIP_TRY(hipMemcpy(dl.ptr, logits, (size_t)n * 4, hipMemcpyHostToDevice));
   HIP_TRY(hipMemcpy(dc.ptr, coins, (size_t)n_draws * 4, hipMemcpyHostToDevice));
   for (int k = 0; k < n_draws; ++k)
     HIP_TRY(launch_sample((const float *)dl.ptr, n, temperature, topp, (const float *)dc.ptr, k, (float *)dp.ptr,
-                          nullptr, nullptr, (int *)dt.ptr, nullptr));
+                          nullptr, nullptr, (int *)dt.ptr, nullptr, nullptr));
   HIP_TRY(hipMemcpy(tokens_out, dt.ptr, (size_t)n_draws * 4, hipMemcpyDeviceToHost));
   return GL3_OK;
 }

@@ -19,7 +19,10 @@
 // the exponent's one per wave) finds the smallest
 // probability the nucleus contains and how many tokens of that probability it
 // takes; a second select finds where the draw falls.  Candidates are visited
-// in descending probability, ties in index order.
+// in descending probability, ties in index order.  The top-p candidates
+// (p >= the cutoff) are listed in index order as the probabilities are formed,
+// so the select passes read that list, not the vocabulary.  After a decode step
+// the maximum logit is read from the step's argmax keys instead of a pass.
 #include "gl3_internal.h"
 
 namespace gl3 {
@@ -146,9 +149,11 @@ __device__ void pick_bin(const unsigned *hcnt, const u64 *hsum, int nb, int sh, 
 // that the mass of the candidates with key > tau is <= target < mass with key
 // >= tau.  The exponent byte's histogram (hecnt/hesum, all candidates) is given;
 // two passes over the candidates with that exponent fix bits [22:11] and [10:0].
-__device__ void radix_select(const float *p, int n, float cutoff, u64 target, const unsigned *hecnt, const u64 *hesum,
-                             unsigned *hcnt, u64 *hsum, u64 *shu, SelectState *st) {
-  const int t = threadIdx.x;
+// The candidates are the compact list cand: wave w's in cand[w R .. w R + ccnt[w]).
+__device__ void radix_select(const float *p, const int *cand, const unsigned *ccnt, int R, u64 target,
+                             const unsigned *hecnt, const u64 *hesum, unsigned *hcnt, u64 *hsum, u64 *shu,
+                             SelectState *st) {
+  const int t = threadIdx.x, wave = t / GL3_WAVE, lane = t % GL3_WAVE;
   if (t == 0) {
     st->prefix = 0u;
     st->mask = 0u;
@@ -171,28 +176,14 @@ __device__ void radix_select(const float *p, int n, float cutoff, u64 target, co
     }
     __syncthreads();
     const unsigned prefix = st->prefix, mask = st->mask;
-    const int n4 = n >> 2;
-#pragma unroll 4
-    for (int g = t; g < n4 + (n & 3 ? 1 : 0); g += SBS) {
-      float q[4];
-      if (g < n4) {
-        const float4 v = ((const float4 *)p)[g];
-        q[0] = v.x;
-        q[1] = v.y;
-        q[2] = v.z;
-        q[3] = v.w;
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) q[j] = 4 * g + j < n ? p[4 * g + j] : -1.0f;
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const unsigned k = key_of(q[j]);
-        if (q[j] >= cutoff && (k & mask) == prefix) {
-          const unsigned b = (k >> sh) & dmask;
-          atomicAdd(&hcnt[b], 1u);
-          atomicAdd(&hsum[b], to_fx(q[j]));
-        }
+    const int c0 = wave * R, c1 = c0 + (int)ccnt[wave];
+    for (int c = c0 + lane; c < c1; c += GL3_WAVE) {
+      const float q = p[cand[c]];
+      const unsigned k = key_of(q);
+      if ((k & mask) == prefix) {
+        const unsigned b = (k >> sh) & dmask;
+        atomicAdd(&hcnt[b], 1u);
+        atomicAdd(&hsum[b], to_fx(q));
       }
     }
     __syncthreads();
@@ -205,9 +196,8 @@ __device__ void radix_select(const float *p, int n, float cutoff, u64 target, co
 // range totals.  The wave whose range holds the crossing stages it in pieces of
 // 16 x 64 weights through LDS and scans lane sub-chunks of 16.
 template <class W>
-__device__ int first_crossing(const W &w, int n, u64 target, const u64 *wt, u64 *piece, int *shi) {
+__device__ int first_crossing_in(const W &w, int r0, int r1, u64 target, const u64 *wt, u64 *piece, int *shi) {
   const int t = threadIdx.x, wave = t / GL3_WAVE, lane = t % GL3_WAVE;
-  const int R = wave_range(n), r0 = wave * R, r1 = min(n, r0 + R);
   if (t == 0) shi[0] = -1;
   __syncthreads();
   u64 before = 0;
@@ -249,19 +239,24 @@ __device__ int first_crossing(const W &w, int n, u64 target, const u64 *wt, u64 
   __syncthreads();
   return shi[0];
 }
+// The same over the waves' ranges of the n elements.
+template <class W>
+__device__ int first_crossing(const W &w, int n, u64 target, const u64 *wt, u64 *piece, int *shi) {
+  const int wave = threadIdx.x / GL3_WAVE;
+  const int R = wave_range(n), r0 = wave * R, r1 = min(n, r0 + R);
+  return first_crossing_in(w, r0, r1, target, wt, piece, shi);
+}
 
 struct FxProb {
   const float *p;
   __device__ __forceinline__ u64 operator()(int i) const { return to_fx(p[i]); }
 };
+// 1 for the candidates (positions in the compact list) whose key is `key`
 struct KeyCount {
   const float *p;
-  float cutoff;
+  const int *cand;
   unsigned key;
-  __device__ __forceinline__ u64 operator()(int i) const {
-    const float q = p[i];
-    return (q >= cutoff && key_of(q) == key) ? 1ull : 0ull;
-  }
+  __device__ __forceinline__ u64 operator()(int c) const { return key_of(p[cand[c]]) == key ? 1ull : 0ull; }
 };
 
 }  // namespace
@@ -272,10 +267,14 @@ struct SampleArgs {
   float temperature, topp;
   const float *coins;   // draws; this call uses coins[coin_index]
   int coin_index;
-  float *probs;         // scratch [n]
+  float *probs;         // scratch [2 n]: the probabilities, then (top-p) the candidates' indices
   int *token_out;       // nullable: the sampled token
   DecodeState *st;      // nullable: the next step forwards the sampled token
   int *rec;             // nullable: rec[coin_index] = the sampled token
+  // nullable (with st): the decode step's argmax keys (the logits' orderable
+  // keys, st->nbest of them at best + (st->parity ^ 1) * st->nbest once the step
+  // has advanced the control block), so the maximum logit needs no pass
+  const unsigned long long *best;
 };
 
 __global__ __launch_bounds__(SBS) void sample_kernel(SampleArgs a) {
@@ -288,6 +287,7 @@ __global__ __launch_bounds__(SBS) void sample_kernel(SampleArgs a) {
   __shared__ u64 shu[SW + 1];
   __shared__ u64 wt[SW];
   __shared__ int shi[4];
+  __shared__ unsigned ccnt[SW];  // top-p: candidates per wave in the compact list
   __shared__ SelectState sel;
   const int t = threadIdx.x, n = a.n, wave = t / GL3_WAVE, lane = t % GL3_WAVE;
   int token = 0;
@@ -315,13 +315,37 @@ __global__ __launch_bounds__(SBS) void sample_kernel(SampleArgs a) {
     float4 *p4 = (float4 *)a.probs;
     const float T = a.temperature;
     float mx = -INFINITY;
+    if (a.best && a.st) {
+      // max_i (l_i / T) = (max_i l_i) / T (division by T > 0 is monotone): the
+      // largest of the step's argmax keys holds the largest logit
+      const int *sv = (const int *)a.st;
+      const int par = ld_coherent_i32(sv + 3), nb = ld_coherent_i32(sv + 5);
+      const unsigned long long *keys = a.best + (size_t)(par ^ 1) * nb;
+      unsigned long long bk = 0;
+      for (int i = t; i < nb; i += SBS) {
+        const unsigned long long k = ld_coherent_u64(keys + i);
+        bk = k > bk ? k : bk;
+      }
+      for (int o = 32; o >= 1; o >>= 1) {
+        const unsigned long long other = __shfl_xor(bk, o);
+        bk = other > bk ? other : bk;
+      }
+      if (lane == 0) shu[wave] = bk;
+      __syncthreads();
+      bk = 0;
+      for (int i = 0; i < SW; ++i) bk = shu[i] > bk ? shu[i] : bk;
+      __syncthreads();
+      const unsigned kb = (unsigned)(bk >> 32);
+      mx = __uint_as_float((kb & 0x80000000u) ? (kb & 0x7fffffffu) : ~kb) / T;
+    } else {
 #pragma unroll 4
-    for (int i = t; i < n4; i += SBS) {
-      const float4 v = l4[i];
-      mx = fmaxf(fmaxf(fmaxf(mx, v.x / T), v.y / T), fmaxf(v.z / T, v.w / T));
+      for (int i = t; i < n4; i += SBS) {
+        const float4 v = l4[i];
+        mx = fmaxf(fmaxf(fmaxf(mx, v.x / T), v.y / T), fmaxf(v.z / T, v.w / T));
+      }
+      for (int i = 4 * n4 + t; i < n; i += SBS) mx = fmaxf(mx, a.logits[i] / T);
+      mx = block_max(mx, shf);
     }
-    for (int i = 4 * n4 + t; i < n; i += SBS) mx = fmaxf(mx, a.logits[i] / T);
-    mx = block_max(mx, shf);
     // the sum in double, rounded once: the float nearest the exact sum of the
     // float exponentials (the reference adds them in float, in index order)
     double s = 0.0;
@@ -348,7 +372,10 @@ __global__ __launch_bounds__(SBS) void sample_kernel(SampleArgs a) {
     // ToppSampler's candidates: p >= (1 - topp) / (n - 1) (ToppSampler.java:63-70)
     const float cutoff = categorical ? 0.0f : (1.0f - topp) / (float)(n - 1);
     // probabilities in place, in the waves' ranges: each wave totals its range's
-    // fixed-point mass (categorical) or histograms its candidates by exponent (top-p)
+    // fixed-point mass (categorical) or histograms its candidates by exponent and
+    // lists their indices, in index order, in cand[r0 ..] (top-p; the later
+    // passes visit the list only: at low temperatures it is a few tokens)
+    int *cand = (int *)(a.probs + n);
     for (int b = t; b < SW * NEXP; b += SBS) {
       hcnt[b] = 0u;
       hsum[b] = 0ull;
@@ -356,6 +383,7 @@ __global__ __launch_bounds__(SBS) void sample_kernel(SampleArgs a) {
     __syncthreads();
     const int R = wave_range(n), r0 = wave * R, r1 = min(n, r0 + R);
     u64 tot = 0;
+    unsigned nc = 0;  // this wave's candidates so far
 #pragma unroll 2
     for (int g = r0 / 4 + lane; g < (r0 + R) / 4; g += GL3_WAVE) {
       float q[4];
@@ -381,6 +409,7 @@ __global__ __launch_bounds__(SBS) void sample_kernel(SampleArgs a) {
           }
         }
       }
+      unsigned mine = 0;  // this lane's candidates (bit j: element 4 g + j)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int i = 4 * g + j;
@@ -390,9 +419,25 @@ __global__ __launch_bounds__(SBS) void sample_kernel(SampleArgs a) {
           const unsigned b = (key_of(q[j]) >> 23) & 0xffu;
           atomicAdd(&hcnt[wave * NEXP + b], 1u);
           atomicAdd(&hsum[wave * NEXP + b], to_fx(q[j]));
+          mine |= 1u << j;
         }
       }
+      if (!categorical) {
+        // lanes in order, each lane's elements in order: index order
+        const unsigned c = (unsigned)__builtin_popcount(mine);
+        unsigned inc = c;
+        for (int o = 1; o < GL3_WAVE; o <<= 1) {
+          const unsigned v = __shfl_up(inc, o);
+          if (lane >= o) inc += v;
+        }
+        unsigned at = nc + inc - c;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (mine & (1u << j)) cand[r0 + at++] = 4 * g + j;
+        nc += __shfl(inc, GL3_WAVE - 1);
+      }
     }
+    if (!categorical && lane == 0) ccnt[wave] = nc;
     if (categorical) {
       tot = wave_sum_u64(tot);
       if (lane == 0) wt[wave] = tot;
@@ -420,7 +465,7 @@ __global__ __launch_bounds__(SBS) void sample_kernel(SampleArgs a) {
       }
       __syncthreads();
       const u64 target = (u64)((double)topp * FX);
-      radix_select(a.probs, n, cutoff, target, hecnt, hesum, hcnt, hsum, shu, &sel);
+      radix_select(a.probs, cand, ccnt, R, target, hecnt, hesum, hcnt, hsum, shu, &sel);
       u64 mass;
       if (sel.found) {
         const u64 ptau = to_fx(__uint_as_float(sel.prefix));
@@ -436,31 +481,32 @@ __global__ __launch_bounds__(SBS) void sample_kernel(SampleArgs a) {
       }
       __syncthreads();
       const u64 r = (u64)((double)coin * (double)mass);
-      radix_select(a.probs, n, cutoff, r, hecnt, hesum, hcnt, hsum, shu, &sel);
+      radix_select(a.probs, cand, ccnt, R, r, hecnt, hesum, hcnt, hsum, shu, &sel);
       token = -1;
+      const int c0 = r0, c1 = r0 + (int)ccnt[wave];  // this wave's part of the candidate list
       if (sel.found) {
         const u64 psig = to_fx(__uint_as_float(sel.prefix));
         const u64 j = psig > 0 ? (r - sel.above) / psig + 1 : 1;
         // the j-th candidate with that probability, in index order
-        const KeyCount kc{a.probs, cutoff, sel.prefix};
+        const KeyCount kc{a.probs, cand, sel.prefix};
         u64 c = 0;
-        for (int i = r0 + lane; i < r1; i += GL3_WAVE) c += kc(i);
+        for (int i = c0 + lane; i < c1; i += GL3_WAVE) c += kc(i);
         c = wave_sum_u64(c);
         __syncthreads();
         if (lane == 0) wt[wave] = c;
         __syncthreads();
-        token = first_crossing(kc, n, j - 1, wt, piece, shi);
+        const int at = first_crossing_in(kc, c0, c1, j - 1, wt, piece, shi);
+        token = at >= 0 ? cand[at] : -1;
       }
       if (token < 0) {
         // rounding only: the last candidate of the walk (the least probable one)
         unsigned long long best = 0;
-        for (int i = t; i < n; i += SBS) {
+        for (int c = c0 + lane; c < c1; c += GL3_WAVE) {
+          const int i = cand[c];
           const float q = a.probs[i];
-          if (q >= cutoff) {
-            // smallest probability, then the largest index (last in the walk order)
-            const unsigned long long k = ((unsigned long long)(~key_of(q)) << 32) | (unsigned)i;
-            best = k > best ? k : best;
-          }
+          // smallest probability, then the largest index (last in the walk order)
+          const unsigned long long k = ((unsigned long long)(~key_of(q)) << 32) | (unsigned)i;
+          best = k > best ? k : best;
         }
         for (int o = 32; o >= 1; o >>= 1) {
           const unsigned long long other = __shfl_xor(best, o);
@@ -487,8 +533,9 @@ __global__ __launch_bounds__(SBS) void sample_kernel(SampleArgs a) {
 }
 
 hipError_t launch_sample(const float *logits, int n, float temperature, float topp, const float *coins, int coin_index,
-                         float *probs, int *token_out, DecodeState *st, int *rec, hipStream_t s) {
-  SampleArgs a{logits, n, temperature, topp, coins, coin_index, probs, token_out, st, rec};
+                         float *probs, int *token_out, DecodeState *st, int *rec, const unsigned long long *best,
+                         hipStream_t s) {
+  SampleArgs a{logits, n, temperature, topp, coins, coin_index, probs, token_out, st, rec, best};
   hipLaunchKernelGGL(sample_kernel, dim3(1), dim3(SBS), 0, s, a);
   return hipGetLastError();
 }
