@@ -1377,10 +1377,10 @@ struct AttTile {
 
 // q, k, v come from m.qkv (plain) or from the tagged cells m.tqkv (TAG, cells
 // written with tag_in); the output goes to m.att or, with tag_out, to m.tatt.
-template <int HD, int GQ, int BS, bool TAG, int RU4 = ATT_RING_U4>
+template <int HD, int GQ, int BS, bool TAG, int RU4 = ATT_RING_U4, class PM = NoTail>
 __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, int nblk, float *lds,
                                 unsigned tag_in = 0, unsigned tag_out = 0, TagWait tw = TagWait{nullptr, 0},
-                                int tk = -1) {
+                                int tk = -1, PM pm = PM{}) {
   constexpr int WPB = BS / GL3_WAVE;
   constexpr int NQ = HD / 8;           // 16-byte chunks of a K row
   constexpr int NC = HD / 32;          // 32-dim chunks (score MFMAs per tile and hi/lo)
@@ -1673,6 +1673,7 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
       }
     }
     if (nsplit == 1) {
+      pm();
 #pragma unroll
       for (int k = 0; k < PAIRS; ++k) {
         const int idx = threadIdx.x + k * BS;
@@ -1712,6 +1713,9 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
       }
     }
     bool merge;
+    // the item's outputs are out: the workgroup's own loads (e.g. the next
+    // phase's weights) may go out ahead of the merge's reads
+    pm();
     if (TAG) {
       // Every split's workgroup merges a slice of the kv head's GQ x hd
       // outputs: float4 groups [sp * gpw, (sp + 1) * gpw), one thread per
