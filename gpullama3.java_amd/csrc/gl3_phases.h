@@ -1510,19 +1510,40 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
           v[r] = v1[0];
         }
       }
+      // head_dim 64 / 128: a head's groups are H4 consecutive lanes of one wave
+      // (heads start at multiples of H4), so the per-head sum and the NeoX
+      // partners move by lane shuffles; head_dim 96 goes through LDS
+      constexpr bool SHFL = (H4 & (H4 - 1)) == 0 && H4 <= GL3_WAVE;
       if (qwen) {
-        // per-head sum of squares: the group partials in dim order
+        float ssh[NG];
+        if constexpr (SHFL) {
+          // butterfly over the head's lanes: every lane ends with the same sum
 #pragma unroll
-        for (int r = 0; r < NG; ++r)
-          if (act[r]) ssb[tg[r]] = ((v[r].x * v[r].x + v[r].y * v[r].y) + v[r].z * v[r].z) + v[r].w * v[r].w;
-        __syncthreads();
+          for (int r = 0; r < NG; ++r) {
+            float ss = act[r] ? ((v[r].x * v[r].x + v[r].y * v[r].y) + v[r].z * v[r].z) + v[r].w * v[r].w : 0.0f;
+#pragma unroll
+            for (int o = H4 / 2; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+            ssh[r] = ss;
+          }
+        } else {
+          // the group partials in dim order
+#pragma unroll
+          for (int r = 0; r < NG; ++r)
+            if (act[r]) ssb[tg[r]] = ((v[r].x * v[r].x + v[r].y * v[r].y) + v[r].z * v[r].z) + v[r].w * v[r].w;
+          __syncthreads();
+#pragma unroll
+          for (int r = 0; r < NG; ++r) {
+            ssh[r] = 0.0f;
+            if (rot[r]) {
+              const int h0 = tg[r] - gi[r] % H4;
+              for (int i = 0; i < H4; ++i) ssh[r] += ssb[h0 + i];
+            }
+          }
+        }
 #pragma unroll
         for (int r = 0; r < NG; ++r)
           if (rot[r]) {
-            const int h0 = tg[r] - gi[r] % H4;
-            float ss = 0.0f;
-            for (int i = 0; i < H4; ++i) ss += ssb[h0 + i];
-            const float si = inv_rms(ss, HD, m.eps);
+            const float si = inv_rms(ssh[r], HD, m.eps);
             v[r].x = w4[r][0] * (si * v[r].x);
             v[r].y = w4[r][1] * (si * v[r].y);
             v[r].z = w4[r][2] * (si * v[r].z);
@@ -1531,15 +1552,29 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
       }
       if (neox) {
         // the partner of dim d is d +- half, in group gi +- H4/2 of the same head
+        float4 pvs[NG];
+        if constexpr (SHFL) {
 #pragma unroll
-        for (int r = 0; r < NG; ++r)
-          if (act[r]) *(float4 *)(qst + 4 * tg[r]) = v[r];
-        __syncthreads();
+          for (int r = 0; r < NG; ++r)
+            pvs[r] = make_float4(__shfl_xor(v[r].x, H4 / 2), __shfl_xor(v[r].y, H4 / 2), __shfl_xor(v[r].z, H4 / 2),
+                                 __shfl_xor(v[r].w, H4 / 2));
+        } else {
+#pragma unroll
+          for (int r = 0; r < NG; ++r)
+            if (act[r]) *(float4 *)(qst + 4 * tg[r]) = v[r];
+          __syncthreads();
+#pragma unroll
+          for (int r = 0; r < NG; ++r) {
+            const bool low = d[r] < half;
+            pvs[r] = rot[r] ? *(const float4 *)(qst + 4 * (low ? tg[r] + H4 / 2 : tg[r] - H4 / 2))
+                            : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+          }
+        }
 #pragma unroll
         for (int r = 0; r < NG; ++r)
           if (rot[r]) {
             const bool low = d[r] < half;
-            const float4 pv = *(const float4 *)(qst + 4 * (low ? tg[r] + H4 / 2 : tg[r] - H4 / 2));
+            const float4 pv = pvs[r];
             float vv[4] = {v[r].x, v[r].y, v[r].z, v[r].w};
             const float pp[4] = {pv.x, pv.y, pv.z, pv.w};
 #pragma unroll
