@@ -113,10 +113,12 @@ def cpu_threads():
     return n
 
 
-def cpu_decode_rate(shape, tensors, starts, per_start, threads):
+def cpu_decode_rate(shape, tensors, starts, per_start, threads, budget_s=0.0):
     """The oracle (C restatement of the reference CPU forward, fp32 KV cache as the
     reference's, OpenMP over rows and heads) decoding `per_start` greedy steps
-    from each start position.  Returns (tok/s, tokens, seconds, algorithmic bytes)."""
+    from each start position; with budget_s, more consecutive steps from each start
+    (as many as the context allows) until about budget_s seconds of decode have run.
+    Returns (tok/s, tokens, seconds, algorithmic bytes)."""
     import oracle.oracle as orc
     from gpullama3_hip.model import tensor_specs
     m = orc.OracleModel(shape, tensors, n_threads=threads)
@@ -124,29 +126,44 @@ def cpu_decode_rate(shape, tensors, starts, per_start, threads):
     m.forward(1, 0)  # thread pool and page warm-up
     n, dt, nbytes = 0, 0.0, 0
     tok = 1
-    for s in starts:
-        for i in range(per_start):
+    taken = [0] * len(starts)
+
+    def run(k, count):
+        nonlocal n, dt, nbytes, tok
+        for _ in range(count):
+            p = starts[k] + taken[k]
+            if p >= shape.context_length:
+                return
             t0 = time.perf_counter()
-            lg = m.forward(tok, s + i)
+            lg = m.forward(tok, p)
             dt += time.perf_counter() - t0
             tok = int(np.argmax(lg))
             n += 1
-            nbytes += wb + kv_bytes(shape, s + i, elem_bytes=4)
+            taken[k] += 1
+            nbytes += wb + kv_bytes(shape, p, elem_bytes=4)
+
+    for k in range(len(starts)):
+        run(k, per_start)
+    if budget_s > dt and n > 0:
+        extra = int(np.ceil((budget_s - dt) / (dt / n) / len(starts)))
+        for k in range(len(starts)):
+            run(k, extra)
     m.close()
     return n / dt, n, dt, nbytes
 
 
-def cpu_baseline(shape, tensors, starts, per_start_all=32, per_start_one=4):
+def cpu_baseline(shape, tensors, starts, per_start_all=32, per_start_one=4, budget_s=12.0):
     """CPU baseline on this host, at the GPU line's segment starts: all cores
-    (the primary figure) and one thread (secondary)."""
+    (the primary figure, a sample of about budget_s seconds) and one thread
+    (secondary)."""
     model, nproc = cpu_info()
     thr = cpu_threads()
-    v_all, n_all, t_all, b_all = cpu_decode_rate(shape, tensors, starts, per_start_all, thr)
+    v_all, n_all, t_all, b_all = cpu_decode_rate(shape, tensors, starts, per_start_all, thr, budget_s)
     v_one, n_one, t_one, b_one = cpu_decode_rate(shape, tensors, starts, per_start_one, 1)
     return {"value": round(v_all, 3), "unit": "tok/s", "cores": thr, "kind": "port",
-            "sample": f"{n_all} greedy decode steps ({per_start_all} from each GPU segment start {list(starts)}) of the "
-                      f"same model: the oracle (C restatement of the reference CPU forward, fp32 KV cache, OpenMP "
-                      f"over rows and heads, AVX2 8-lane dots), {t_all:.1f} s",
+            "sample": f"{n_all} greedy decode steps (consecutive positions from each GPU segment start "
+                      f"{list(starts)}) of the same model: the oracle (C restatement of the reference CPU forward, "
+                      f"fp32 KV cache, OpenMP over rows and heads, AVX2 8-lane dots), {t_all:.1f} s",
             "cpu_model": model, "nproc": nproc, "threads": thr,
             "achieved_gbs": round(b_all / t_all / 1e9, 2),
             "one_thread": {"value": round(v_one, 3), "unit": "tok/s", "steps": n_one, "seconds": round(t_one, 2),
