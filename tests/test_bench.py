@@ -83,3 +83,20 @@ def test_segments_reject_what_does_not_fit():
         bench.segments("llama1b_q8", 0, 2304)
     with pytest.raises(ValueError):
         bench.segments("llama1b_q8", 2048, 2304)
+
+
+def test_cpu_baseline_sample_stays_inside_the_context():
+    """The CPU baseline decodes per_start steps from each start, then, with a time
+    budget, further consecutive positions only up to the context's end."""
+    from gpullama3_hip.model import synth_model
+    from tests.harness import small
+    shape = small("llama1b_q8", vocab=512, ctx=64)
+    tensors = synth_model(shape, 3)
+    wb = bench.weight_bytes(shape, tensor_specs(shape))
+    _, n, _, nbytes = bench.cpu_decode_rate(shape, tensors, [0, 40], 4, 1)
+    assert n == 8
+    assert nbytes == 8 * wb + sum(bench.kv_bytes(shape, p, elem_bytes=4) for p in [0, 1, 2, 3, 40, 41, 42, 43])
+    # a budget far beyond what the context allows: every position from the start to the end, once
+    _, n, _, nbytes = bench.cpu_decode_rate(shape, tensors, [52], 4, 1, budget_s=1e4)
+    assert n == 12
+    assert nbytes == 12 * wb + sum(bench.kv_bytes(shape, p, elem_bytes=4) for p in range(52, 64))
