@@ -235,6 +235,7 @@ typedef Shape<FMT_Q8,  4096, 4096, 1024, 14336, 128, 4, 8, 2, Tile<4, 1, 2>, Til
 typedef Shape<FMT_Q8,  3072, 3072, 1024,  8192, 128, 3, 8, 2, Tile<3, 1, 2>, Tile<3, 1, 2>, Tile<3, 1, 1>, Tile<4, 2, 1>, Tile<3, 1, 2>> ShapeLlama3BQ8;
 typedef Shape<FMT_Q8,  3072, 3072, 3072,  8192,  96, 1, 8, 2, Tile<3, 1, 2>, Tile<3, 1, 2>, Tile<3, 1, 1>, Tile<4, 2, 1>, Tile<3, 1, 2>> ShapePhi3MiniQ8;
 typedef Shape<FMT_F16, 4096, 4096, 1024, 14336, 128, 4, 8, 3, Tile<8, 1, 1>, Tile<8, 1, 1>, Tile<4, 2, 1>, Tile<7, 4, 1>, Tile<8, 1, 1>> ShapeMistral7BF16;
+typedef Shape<FMT_F16, 2560, 4096, 1024,  9728, 128, 4, 8, 3, Tile<5, 1, 1>, Tile<4, 2, 1>, Tile<5, 1, 1>, Tile<19, 1, 1>, Tile<5, 1, 1>> ShapeQwen3_4BF16;
 
 // The fused FFN's Wdown slice (two slot-loads), requested into ring slots 0
 // and 1 as soon as gate/up's dot products are done with them, so it streams
@@ -450,6 +451,7 @@ bool find_step_kernel(const ModelDev &m, int grid, StepKernel *out) {
   if (shape_matches<ShapeLlama3BQ8>(m)) { *out = make_step_kernel<ShapeLlama3BQ8>(m, grid); return true; }
   if (shape_matches<ShapePhi3MiniQ8>(m)) { *out = make_step_kernel<ShapePhi3MiniQ8>(m, grid); return true; }
   if (shape_matches<ShapeMistral7BF16>(m)) { *out = make_step_kernel<ShapeMistral7BF16>(m, grid); return true; }
+  if (shape_matches<ShapeQwen3_4BF16>(m)) { *out = make_step_kernel<ShapeQwen3_4BF16>(m, grid); return true; }
   return false;
 }
 
