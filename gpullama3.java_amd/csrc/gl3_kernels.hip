@@ -201,7 +201,10 @@ hipError_t launch_finish(const ModelDev &m, hipStream_t s) {
 // GEMV phase lists its tile (KC chunks per lane, KS waves splitting K, NR rows
 // per wave) for 4-wave workgroups, chosen so that a wave's tile fills one ring
 // slot of SC chunks and the work items of every phase spread evenly over the
-// CUs.  DEPTH ring slots per wave are in flight.
+// CUs.  DEPTH ring slots per wave are in flight.  Qwen3-4B FP16 (K = 2560: five
+// 512-element rounds per row) takes 12-chunk slots so that a gate/up row pair
+// is one slot-load, two of them in flight, and two K/V tiles in flight in the
+// attention phase, which keeps the ring within LDS.
 template <int KC_, int KS_, int NR_>
 struct Tile {
   static constexpr int KC = KC_, KS = KS_, NR = NR_;
@@ -212,10 +215,11 @@ struct Tile {
 // gate/up tiles such that a workgroup's 32 rows are four slot-loads (held in
 // ring slots 0..3 at once).
 template <int FMT_, int DIM, int QD, int KVD, int HID, int HD, int G, int SC, int DEPTH, class TQKV, class TWO,
-          class TGU, class TDN, class TCLS, int FFN = 0>
+          class TGU, class TDN, class TCLS, int FFN = 0, int ATTD = ATT_DEPTH>
 struct Shape {
   static constexpr int fmt = FMT_, dim = DIM, q_dim = QD, kv_dim = KVD, hidden = HID, hd = HD, gqa = G;
   static constexpr int ffn = FFN;
+  static constexpr int att_depth = ATTD;  // K/V tiles in flight per wave in the attention phase
   static constexpr int BS = GL3_STEP_BLOCK;
   typedef GemvPhase<FMT_, TQKV::KC, TQKV::KS, TQKV::NR, MODE_STORE, BS, SC, DEPTH> QKV;
   typedef GemvPhase<FMT_, TWO::KC, TWO::KS, TWO::NR, MODE_RESIDUAL, BS, SC, DEPTH> WO;
@@ -235,7 +239,7 @@ typedef Shape<FMT_Q8,  4096, 4096, 1024, 14336, 128, 4, 8, 2, Tile<4, 1, 2>, Til
 typedef Shape<FMT_Q8,  3072, 3072, 1024,  8192, 128, 3, 8, 2, Tile<3, 1, 2>, Tile<3, 1, 2>, Tile<3, 1, 1>, Tile<4, 2, 1>, Tile<3, 1, 2>> ShapeLlama3BQ8;
 typedef Shape<FMT_Q8,  3072, 3072, 3072,  8192,  96, 1, 8, 2, Tile<3, 1, 2>, Tile<3, 1, 2>, Tile<3, 1, 1>, Tile<4, 2, 1>, Tile<3, 1, 2>> ShapePhi3MiniQ8;
 typedef Shape<FMT_F16, 4096, 4096, 1024, 14336, 128, 4, 8, 3, Tile<8, 1, 1>, Tile<8, 1, 1>, Tile<4, 2, 1>, Tile<7, 4, 1>, Tile<8, 1, 1>> ShapeMistral7BF16;
-typedef Shape<FMT_F16, 2560, 4096, 1024,  9728, 128, 4, 8, 3, Tile<5, 1, 1>, Tile<4, 2, 1>, Tile<5, 1, 1>, Tile<19, 1, 1>, Tile<5, 1, 1>> ShapeQwen3_4BF16;
+typedef Shape<FMT_F16, 2560, 4096, 1024,  9728, 128, 4, 12, 2, Tile<5, 1, 2>, Tile<2, 4, 5>, Tile<5, 1, 1>, Tile<19, 1, 1>, Tile<5, 1, 2>, 0, 2> ShapeQwen3_4BF16;
 
 // The fused FFN's Wdown slice (two slot-loads), requested into ring slots 0
 // and 1 as soon as gate/up's dot products are done with them, so it streams
@@ -307,12 +311,12 @@ __global__ __launch_bounds__(GL3_STEP_BLOCK, 1) void decode_step_kernel(ModelDev
       // attention streams K/V through the GEMV ring: Wo's tiles are requested after it
       // (two stamps inside: q/k/v read, tiles done)
       if constexpr (SH::ffn == 1)
-        phase_attention<SH::hd, SH::gqa, SH::BS, true, SH::QKV::WCH>(
+        phase_attention<SH::hd, SH::gqa, SH::BS, true, SH::QKV::WCH, SH::att_depth>(
             m, l, si.pos, blk, nblk, lds, t_qkv, t_att, tw, m.tstamp ? tk : -1,
             GateUpAfterAttention<typename SH::GU>{ld_mat(&L->gu), SH::hidden, blk, nblk});
       else
-        phase_attention<SH::hd, SH::gqa, SH::BS, true, SH::QKV::WCH>(m, l, si.pos, blk, nblk, lds, t_qkv, t_att, tw,
-                                                                    m.tstamp ? tk : -1);
+        phase_attention<SH::hd, SH::gqa, SH::BS, true, SH::QKV::WCH, SH::att_depth>(
+            m, l, si.pos, blk, nblk, lds, t_qkv, t_att, tw, m.tstamp ? tk : -1);
       tk += 2;
       trace(m, tk++);
       // workgroups without an attention item wait quietly for the attention output

@@ -1156,7 +1156,7 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-#define ATT_DEPTH 3  // K/V ring slots per wave (2 or 3)
+#define ATT_DEPTH 3  // K/V ring slots per wave (2 or 3; a shape may choose 2 to free LDS)
 #define ATT_RING_U4 (4 * 8 * GL3_WAVE)  // default ring slot (4 waves x 8 KB), in u32x4
 
 __device__ __forceinline__ void rope_pair(float &v0, float &v1, float c, float s) {
@@ -1206,7 +1206,7 @@ __device__ __forceinline__ float inv_rms(float ss, int hd, float eps) {
 // the compiler's own wait counts do not serialize the slots.
 // RU4: ring slot size in u32x4 (the GEMV phases' slot in the persistent
 // kernel, so both use one ring); a wave's tile needs 4 hd of them.
-template <int HD, int GQ, int RU4>
+template <int HD, int GQ, int RU4, int AD = ATT_DEPTH>
 struct AttTile {
   static_assert(RU4 >= 16 * HD, "ring slot too small for a K/V tile per wave");
   static constexpr int NQ = HD / 8, NC = HD / 32, NB = HD / 16, NKI = HD / 32, NVI = HD / 32, NI = NKI + NVI;
@@ -1249,14 +1249,14 @@ struct AttTile {
     if (u >= ntw) return;
     // slot S is complete once at most the loads of the later issued tiles are outstanding
     const int later = ntw - 1 - u;
-    if (ATT_DEPTH >= 3 && later >= 2)
+    if (AD >= 3 && later >= 2)
       wait_vmem<2 * NI>();
     else if (later == 1)
       wait_vmem<NI>();
     else
       wait_vmem<0>();
     tile<S>(u, qh, ql, knb, vnb, O, mrun, lrun);
-    if (u + ATT_DEPTH < ntw) issue<S>(u + ATT_DEPTH);
+    if (u + AD < ntw) issue<S>(u + AD);
   }
 
   template <int S>
@@ -1377,7 +1377,7 @@ struct AttTile {
 
 // q, k, v come from m.qkv (plain) or from the tagged cells m.tqkv (TAG, cells
 // written with tag_in); the output goes to m.att or, with tag_out, to m.tatt.
-template <int HD, int GQ, int BS, bool TAG, int RU4 = ATT_RING_U4, class PM = NoTail>
+template <int HD, int GQ, int BS, bool TAG, int RU4 = ATT_RING_U4, int AD = ATT_DEPTH, class PM = NoTail>
 __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, int nblk, float *lds,
                                 unsigned tag_in = 0, unsigned tag_out = 0, TagWait tw = TagWait{nullptr, 0},
                                 int tk = -1, PM pm = PM{}) {
@@ -1421,7 +1421,7 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
     uint16_t *vbase = m.vc + ((size_t)layer * m.n_kv + kvh) * HD * m.ctxp;
     const dma_rsrc_t rk = rsrc(kbase), rv = rsrc(vbase);
 
-    AttTile<HD, GQ, RU4> at;
+    AttTile<HD, GQ, RU4, AD> at;
     at.m = &m;
     at.rk = rk;
     at.rv = rv;
@@ -1598,7 +1598,7 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
         if (act[r]) *(float4 *)(qrot + 4 * tg[r]) = v[r];
       __syncthreads();
       if (ntw > 1) at.template issue<1, true>(1);
-      if (ATT_DEPTH >= 3 && ntw > 2) at.template issue<(ATT_DEPTH >= 3 ? 2 : 1), true>(2);
+      if (AD >= 3 && ntw > 2) at.template issue<(AD >= 3 ? 2 : 1), true>(2);
     }
     if (tk >= 0 && item == blk) trace(m, tk);
     // q of head hh (columns >= GQ take head 0 and keep zeros) as fp16 hi + lo
@@ -1640,10 +1640,10 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
 #pragma unroll
     for (int b = 0; b < NB; ++b) O[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     float mrun = -INFINITY, lrun = 0.0f;
-    for (int u = 0; u < ntw; u += ATT_DEPTH) {
+    for (int u = 0; u < ntw; u += AD) {
       at.template step<0>(u, ntw, qh, ql, knb, vnb, O, mrun, lrun);
       at.template step<1>(u + 1, ntw, qh, ql, knb, vnb, O, mrun, lrun);
-      if (ATT_DEPTH >= 3) at.template step<(ATT_DEPTH >= 3 ? 2 : 1)>(u + 2, ntw, qh, ql, knb, vnb, O, mrun, lrun);
+      if (AD >= 3) at.template step<(AD >= 3 ? 2 : 1)>(u + 2, ntw, qh, ql, knb, vnb, O, mrun, lrun);
     }
     if (wave == wpos && lane < NQ) {
       // append the new row to the cache, after the tiles: the stores count in
