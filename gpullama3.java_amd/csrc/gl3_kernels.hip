@@ -310,17 +310,17 @@ __global__ __launch_bounds__(GL3_STEP_BLOCK, 1) void decode_step_kernel(ModelDev
       trace(m, tk++);
       // attention streams K/V through the GEMV ring: Wo's tiles are requested after it
       // (two stamps inside: q/k/v read, tiles done)
+      const int msplit = att_tag_splits(m, si.pos + 1, nblk, SH::ffn == 1);
       if constexpr (SH::ffn == 1)
         phase_attention<SH::hd, SH::gqa, SH::BS, true, SH::QKV::WCH, SH::att_depth>(
             m, l, si.pos, blk, nblk, lds, t_qkv, t_att, tw, m.tstamp ? tk : -1,
-            GateUpAfterAttention<typename SH::GU>{ld_mat(&L->gu), SH::hidden, blk, nblk});
+            GateUpAfterAttention<typename SH::GU>{ld_mat(&L->gu), SH::hidden, blk, nblk}, msplit);
       else
         phase_attention<SH::hd, SH::gqa, SH::BS, true, SH::QKV::WCH, SH::att_depth>(
-            m, l, si.pos, blk, nblk, lds, t_qkv, t_att, tw, m.tstamp ? tk : -1);
+            m, l, si.pos, blk, nblk, lds, t_qkv, t_att, tw, m.tstamp ? tk : -1, NoTail{}, msplit);
       tk += 2;
       trace(m, tk++);
       // workgroups without an attention item wait quietly for the attention output
-      const int msplit = max(1, min(min(m.max_split, 64), nblk / m.n_kv));
       const int S = att_split_len(si.pos + 1, msplit, 16 * (SH::BS / GL3_WAVE));
       const bool att_wg = blk < m.n_kv * ((si.pos + S) / S);
       SH::WO::prefetch(ld_mat(&L->wo), SH::dim, blk, nblk);

@@ -1377,10 +1377,22 @@ struct AttTile {
 
 // q, k, v come from m.qkv (plain) or from the tagged cells m.tqkv (TAG, cells
 // written with tag_in); the output goes to m.att or, with tag_out, to m.tatt.
+// Splits per kv head of the attention phase inside the persistent kernel (n
+// positions): at most one item per workgroup and 64 splits per head.  With the
+// fused FFN, whose workgroups without an item request gate/up's weights during
+// attention, at most half the workgroups hold an item once a split would pass
+// 48 positions (Llama-3.2-1B Q8_0: -1.3% / -2.5% time per token at positions
+// 1728 / 2016; halving at every length costs +1.3% at 1152).
+__device__ __forceinline__ int att_tag_splits(const ModelDev &m, int n, int nblk, bool fused) {
+  int ms = max(1, min(min(m.max_split, 64), nblk / m.n_kv));
+  if (fused && n > 48 * ms) ms = max(1, ms / 2);
+  return ms;
+}
+
 template <int HD, int GQ, int BS, bool TAG, int RU4 = ATT_RING_U4, int AD = ATT_DEPTH, class PM = NoTail>
 __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, int nblk, float *lds,
                                 unsigned tag_in = 0, unsigned tag_out = 0, TagWait tw = TagWait{nullptr, 0},
-                                int tk = -1, PM pm = PM{}) {
+                                int tk = -1, PM pm = PM{}, int msplit_tag = 0) {
   constexpr int WPB = BS / GL3_WAVE;
   constexpr int NQ = HD / 8;           // 16-byte chunks of a K row
   constexpr int NC = HD / 32;          // 32-dim chunks (score MFMAs per tile and hi/lo)
@@ -1388,8 +1400,8 @@ __device__ void phase_attention(const ModelDev &m, int layer, int pos, int blk, 
   static_assert(WPB == 4 && HD % 32 == 0 && HD <= 128 && GQ <= 8, "attention tile shape");
   const int hd = HD, half = HD / 2;
   const int n = pos + 1;
-  // tagged merge: at most one item per workgroup and 64 splits per head
-  const int msplit = TAG ? max(1, min(min(m.max_split, 64), nblk / m.n_kv)) : m.max_split;
+  // tagged merge: at most one item per workgroup (the caller's split count)
+  const int msplit = TAG ? (msplit_tag > 0 ? msplit_tag : att_tag_splits(m, n, nblk, false)) : m.max_split;
   const int S = att_split_len(n, msplit, 16 * WPB);
   const int nsplit = (n + S - 1) / S;
   const int items = m.n_kv * nsplit;
