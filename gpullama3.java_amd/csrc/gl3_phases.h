@@ -1247,11 +1247,12 @@ struct AttTile {
                                        const unsigned (&knb)[4], const unsigned (&vnb)[4], f32x4 (&O)[NB],
                                        float &mrun, float &lrun) const {
     if (u >= ntw) return;
-    // slot S is complete once at most the loads of the later issued tiles are outstanding
+    // slot S is complete once at most the loads of the later issued tiles are
+    // outstanding: min(later, AD - 1) tiles
     const int later = ntw - 1 - u;
     if (AD >= 3 && later >= 2)
       wait_vmem<2 * NI>();
-    else if (later == 1)
+    else if (later >= 1)
       wait_vmem<NI>();
     else
       wait_vmem<0>();

@@ -14,7 +14,7 @@ from gpullama3_hip import HipMasterPlan
 from gpullama3_hip import _lib as L
 from gpullama3_hip.gguf import write_gguf
 from gpullama3_hip.model import synth_model
-from harness import build, prefill_kv, small, top2_margin
+from harness import build, prefill_from_device, prefill_kv, small, top2_margin
 
 pytestmark = pytest.mark.gpu
 
@@ -52,6 +52,27 @@ def test_decode_matches_oracle(gpu, key, sched):
         print(f"  max|d|/std = {d:.2e}", flush=True)
         assert d <= TOL_TIGHT, d
         assert am == int(np.argmax(lg))
+        if top2_margin(rl) > TOL_TIGHT * rl.std():
+            assert am == orc.argmax(rl)
+    plan.free_execution_plan()
+    ref.close()
+
+
+@pytest.mark.parametrize("sched", sorted(SCHEDULES))
+def test_two_tile_attention_ring_at_long_context(gpu, sched):
+    """Qwen3-4B FP16, whose persistent kernel keeps two K/V tiles in flight per
+    wave: positions past 7000, where a split spans four tiles per wave (the
+    waits then count one tile issued ahead), against the oracle."""
+    shape = small("qwen3_4b_f16", ctx=8192)
+    print(f"[case] qwen3_4b_f16 {sched} at 7000+", flush=True)
+    plan, ref, _ = build(shape, flags=SCHEDULES[sched], kv_fp16=True)
+    prefill_from_device(plan, ref, shape, 7000)
+    rng = np.random.default_rng(13)
+    toks = rng.integers(0, shape.vocab_size, 3)
+    for lg, am, rl in run_steps(plan, ref, toks, np.arange(7000, 7003)):
+        d = np.max(np.abs(lg - rl)) / rl.std()
+        print(f"  max|d|/std = {d:.2e}", flush=True)
+        assert d <= TOL_TIGHT, d
         if top2_margin(rl) > TOL_TIGHT * rl.std():
             assert am == orc.argmax(rl)
     plan.free_execution_plan()
