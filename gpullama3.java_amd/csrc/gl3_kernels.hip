@@ -237,7 +237,7 @@ typedef Shape<FMT_Q8,  1024, 2048, 1024,  3072, 128, 2, 8, 3, Tile<1, 1, 4>, Til
 typedef Shape<FMT_F16, 3072, 3072, 3072,  8192,  96, 1, 8, 3, Tile<6, 1, 1>, Tile<6, 1, 1>, Tile<3, 2, 1>, Tile<4, 4, 2>, Tile<6, 1, 1>> ShapePhi3MiniF16;
 typedef Shape<FMT_Q8,  4096, 4096, 1024, 14336, 128, 4, 8, 2, Tile<4, 1, 2>, Tile<4, 1, 2>, Tile<4, 1, 1>, Tile<7, 2, 1>, Tile<4, 1, 2>> ShapeLlama8BQ8;
 typedef Shape<FMT_Q8,  3072, 3072, 1024,  8192, 128, 3, 8, 2, Tile<3, 1, 2>, Tile<3, 1, 2>, Tile<3, 1, 1>, Tile<4, 2, 1>, Tile<3, 1, 2>> ShapeLlama3BQ8;
-typedef Shape<FMT_Q8,  3072, 3072, 3072,  8192,  96, 1, 8, 2, Tile<3, 1, 2>, Tile<3, 1, 2>, Tile<3, 1, 1>, Tile<4, 2, 1>, Tile<3, 1, 2>> ShapePhi3MiniQ8;
+typedef Shape<FMT_Q8,  3072, 3072, 3072,  8192,  96, 1, 8, 2, Tile<3, 1, 1>, Tile<3, 1, 1>, Tile<3, 1, 1>, Tile<4, 2, 1>, Tile<3, 1, 2>> ShapePhi3MiniQ8;
 typedef Shape<FMT_F16, 4096, 4096, 1024, 14336, 128, 4, 8, 3, Tile<8, 1, 1>, Tile<8, 1, 1>, Tile<4, 2, 1>, Tile<7, 4, 1>, Tile<8, 1, 1>> ShapeMistral7BF16;
 typedef Shape<FMT_F16, 2560, 4096, 1024,  9728, 128, 4, 12, 2, Tile<5, 1, 2>, Tile<2, 4, 5>, Tile<5, 1, 1>, Tile<19, 1, 1>, Tile<5, 1, 2>, 0, 2> ShapeQwen3_4BF16;
 
