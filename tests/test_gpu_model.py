@@ -79,6 +79,26 @@ def test_two_tile_attention_ring_at_long_context(gpu, sched):
     ref.close()
 
 
+def test_attention_split_count_switch(gpu):
+    """The fused-FFN shape halves its attention splits once a split would pass
+    48 positions (1536 positions with 32 splits of a kv head): decode steps across
+    the switch against the oracle."""
+    shape = small("llama1b_q8", ctx=2048)
+    print("[case] llama1b_q8 split switch at 1536", flush=True)
+    plan, ref, _ = build(shape, kv_fp16=True)
+    prefill_from_device(plan, ref, shape, 1532)
+    rng = np.random.default_rng(17)
+    toks = rng.integers(0, shape.vocab_size, 8)
+    for lg, am, rl in run_steps(plan, ref, toks, np.arange(1532, 1540)):
+        d = np.max(np.abs(lg - rl)) / rl.std()
+        print(f"  max|d|/std = {d:.2e}", flush=True)
+        assert d <= TOL_TIGHT, d
+        if top2_margin(rl) > TOL_TIGHT * rl.std():
+            assert am == orc.argmax(rl)
+    plan.free_execution_plan()
+    ref.close()
+
+
 @pytest.mark.parametrize("key", ["llama1b_q8", "qwen3_06b_q8"])
 def test_decode_vs_reference_fp32_kv(gpu, key):
     shape = small(key)
